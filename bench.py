@@ -1,0 +1,214 @@
+"""Benchmark: BCJR fwd+bwd trellis state-updates/s on one MI355X.
+
+Workload (default): the single-tile kernel config -- L=16 (65,536 states), k=2,
+V=1, 256 steps, 4,096 sequences (one 1024x1024 float32 N(0,1) matrix in 16x16
+tiles), 3INST codebook, T=0.1.  One step = forward (soft codewords) + backward
+(gradient wrt the sequences) of the BCJR node over the whole batch, with inputs
+resident in HBM.  State-updates per step = 4 sweeps (alpha, beta and the two
+adjoint sweeps) x B x N x 2^L cells; recompute sweeps are not counted.
+
+Also reported: per-kernel durations from HIP events on the launch stream, the
+roofline of the dominant kernel against the measured v_exp_f32 issue rate, and
+the CPU oracle (C/OpenMP) timed on a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config tile|cpu|layer]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "quant-2bit_amd"))
+sys.path.insert(0, ROOT)
+
+# Algorithmic transcendentals per cell (exp2/log2), structure-aware count:
+#   soft pass: alpha-LSE exp + beta-LSE exp + marginal exp + one log per 2^kV group per sweep
+#   fwd+grad : the soft pass plus one exp per cell for each adjoint sweep
+def trans_per_cell_soft(kV):
+    return 3.0 + 2.0 * 2.0 ** (-kV)
+
+
+def trans_per_cell_grad(kV):
+    return 5.0 + 2.0 * 2.0 ** (-kV)
+
+
+LAYER_SEQS = 237_568  # Llama-3.2-1B decoder layer: q,o 2048^2; k,v 512x2048; MLP 3x8192x2048
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="tile", choices=["tile", "cpu", "layer"])
+    ap.add_argument("--T", type=float, default=0.1)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=24, help="sequences in the CPU baseline sample")
+    return ap.parse_args()
+
+
+def measure_peaks(torch, dev):
+    """v_exp_f32 / v_log_f32 / v_fma_f32 issue rates (per second, whole chip)."""
+    import bcjr
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(bcjr.LIB_PATH), "libbcjr_peak.so"))
+    lib.bcjr_peak_launch.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_void_p]
+    chains = lib.bcjr_peak_chains()
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    blocks = n_cu * 16  # 16 waves of 64 per CU (4 per SIMD)
+    sink = torch.empty(blocks * 256, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    out = {}
+
+    def run(kind, K, iters):
+        rc = lib.bcjr_peak_launch(kind, K, sink.data_ptr(), blocks, iters, ctypes.c_void_p(stream.cuda_stream))
+        assert rc == 0, rc
+
+    for name, kind, K, per_iter in (("exp", 0, 0, 1), ("log", 1, 0, 1), ("fma", 2, 0, 1),
+                                    ("exp+2fma", 3, 2, 1), ("exp+4fma", 3, 4, 1)):
+        iters = 4096
+        run(kind, K, 64)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        run(kind, K, iters)
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        sec = e0.elapsed_time(e1) / 1e3
+        ops = blocks * 256.0 * chains * iters * per_iter
+        out[name] = {"per_s": ops / sec, "ms": sec * 1e3}
+    return out
+
+
+def cpu_baseline(seq, g, cb_np, T, L, kV, sample):
+    import numpy as np
+    import oracle
+    threads = len(os.sched_getaffinity(0))
+    threads = min(threads, 16)
+    oracle.num_threads(threads)
+    s = seq[:sample]
+    gg = g[:sample]
+    t0 = time.perf_counter()
+    oracle.bcjr_forward(s, cb_np, T, L, kV, nthreads=threads)
+    oracle.bcjr_backward(s, cb_np, T, L, kV, gg, nthreads=threads)
+    dt = time.perf_counter() - t0
+    cells = sample * s.shape[1] * (1 << L)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": 4.0 * cells / dt, "unit": "state-updates/s", "cores": threads, "kind": "port",
+            "seconds": dt,
+            "sample": f"{sample} of the workload's sequences, fwd+bwd, C/OpenMP float64 oracle "
+                      f"(oracle/bcjr_oracle.c), {cpu_model}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards "
+              "across GPUs by sequences with no collective inside BCJR.", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    import bcjr
+    from bcjr import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.config == "tile":
+        L, k, V, N, B, kind = 16, 2, 1, 256, 4096, "3inst"
+        workload = "single-tile: L=16 k=2 V=1 N=256 B=4096 (1024x1024 matrix), 3INST, T=%g" % args.T
+    elif args.config == "cpu":
+        L, k, V, N, B, kind = 12, 2, 1, 256, 128, "1mad"
+        workload = "cpu-config: L=12 k=2 V=1 N=256 B=128, 1MAD, T=%g" % args.T
+    else:
+        L, k, V, N, B, kind = 16, 2, 1, 256, LAYER_SEQS, "3inst"
+        workload = "llama-3.2-1b layer: L=16 k=2 V=1 N=256 B=237568, 3INST, T=%g" % args.T
+    kV = k * V
+    rng = np.random.default_rng(0)
+    seq_np = rng.standard_normal((B, N, V)).astype(np.float32)
+    g_np = np.random.default_rng(1).standard_normal((B, N, V)).astype(np.float32)
+    cb = bcjr.make_3inst_codebook(L, dev) if kind == "3inst" else bcjr.make_1mad_codebook(L, dev)
+    x = torch.tensor(seq_np, device=dev)
+    g = torch.tensor(g_np, device=dev)
+    spec, _ = bcjr.forward_backward._spec_for(cb, L, k, V)
+
+    def step():
+        xs = x.detach().requires_grad_(True)
+        soft, _ = bcjr.bcjr_forward_backward(xs, cb, args.T, L=L, k=k, V=V)
+        soft.backward(g)
+        return xs.grad
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    ms_step = wall / args.steps * 1e3
+    cells = float(B) * N * (1 << L)
+    value = 4.0 * cells / (wall / args.steps)
+
+    # Per-kernel durations (HIP events on the stream the kernels run on).
+    stream = torch.cuda.current_stream(dev)
+    reps = max(2, min(args.steps, 5))
+    t_f, t_b = [], []
+    for _ in range(reps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        e[0].record(stream)
+        ops.forward(spec, x, args.T, None)
+        e[1].record(stream)
+        e[2].record(stream)
+        ops.backward(spec, x, args.T, None, g)
+        e[3].record(stream)
+        torch.cuda.synchronize(dev)
+        t_f.append(e[0].elapsed_time(e[1]) / 1e3)
+        t_b.append(e[2].elapsed_time(e[3]) / 1e3)
+    fwd_s, bwd_s = sum(t_f) / reps, sum(t_b) / reps
+
+    peaks = measure_peaks(torch, dev)
+    exp_peak = peaks["exp"]["per_s"]
+    dominant = "bcjr_bwd_kernel" if bwd_s >= fwd_s else "bcjr_fwd_kernel"
+    per_cell = trans_per_cell_grad(kV) if dominant == "bcjr_bwd_kernel" else trans_per_cell_soft(kV)
+    dur = bwd_s if dominant == "bcjr_bwd_kernel" else fwd_s
+    achieved = per_cell * cells / dur
+    roofline = {
+        "bound": "valu_exp", "kernel": dominant,
+        "achieved": achieved / 1e12, "peak": exp_peak / 1e12, "unit": "Texp/s",
+        "frac": achieved / exp_peak, "traffic": None,
+        "per_cell": per_cell, "cells": cells, "launch_s": dur,
+    }
+    kernels = {
+        "bcjr_fwd_kernel": {"ms": fwd_s * 1e3, "algorithmic_Texp_s": trans_per_cell_soft(kV) * cells / fwd_s / 1e12},
+        "bcjr_bwd_kernel": {"ms": bwd_s * 1e3, "algorithmic_Texp_s": trans_per_cell_grad(kV) * cells / bwd_s / 1e12},
+    }
+    layer_cells = float(LAYER_SEQS) * 256 * 65536
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(seq_np, g_np, cb.cpu().numpy(), args.T, L, kV, min(args.cpu_sample, B))
+
+    line = {
+        "metric": "BCJR fwd+bwd state-updates/sec (L=16,k=2); s per Llama-1B layer QAT step",
+        "value": value, "unit": "state-updates/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic N(0,1) sequences (seed 0), upstream gradient N(0,1) (seed 1)",
+        "config": {"workload": workload, "L": L, "k": k, "V": V, "N": N, "B": B, "code": kind, "T": args.T},
+        "layer_step_s_est": 4.0 * layer_cells / value,
+        "roofline": roofline, "kernels": kernels,
+        "peaks_per_s": {k_: v["per_s"] for k_, v in peaks.items()},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,310 @@
+"""CPU oracle for the BCJR forward-backward path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this package, and only as the checker (or the timed CPU
+baseline).  The product path under ``quant-2bit_amd/`` never imports it.
+
+Contents
+--------
+``lib()``                 ctypes handle on ``oracle/_build/libbcjr_oracle.so``, the
+                          C restatement (``bcjr_oracle.c``) of the reference's
+                          eager BCJR node, gradient and Viterbi encoder.
+``codebook / bcjr_forward / bcjr_backward / viterbi / decode``
+                          numpy-facing wrappers over the C restatement.
+``naive_forward``         literal numpy restatement of the reference's eager
+                          algorithm (gather over predecessor tables, then
+                          logsumexp), src/bcjr/forward_backward.py:62-232.
+``brute_force``           exhaustive path enumeration (tiny trellises only): exact
+                          logZ, soft codeword and gradient (as the posterior
+                          covariance of the codeword sequence), plus the
+                          min-cost path.  Pins the recursions independently of
+                          their form.
+``pack_bits / unpack_bits``
+                          2-bit (k*V-bit) LSB-first packing of per-step indices.
+
+Parity status of each restatement is listed in ``oracle/PINNING.md``.
+"""
+from __future__ import annotations
+
+import ctypes
+import itertools
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libbcjr_oracle.so")
+_lib = None
+
+CODE_TABLE, CODE_1MAD, CODE_3INST, CODE_HYB = 0, 1, 2, 3
+
+
+def build(force: bool = False) -> str:
+    """Compile the C restatement with oracle/Makefile (gcc -O2 -fopenmp)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.check_call(["make", "-s", "-C", _HERE], stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        i32, i64, fp = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+        L.oracle_codebook.argtypes = [i32, i32, fp, i32, fp]
+        L.oracle_bcjr_forward.argtypes = [i32, i32, i32, i64, i32, fp, fp, i32, fp, fp, fp, i32]
+        L.oracle_bcjr_backward.argtypes = [i32, i32, i32, i64, i32, fp, fp, i32, fp, fp, fp, fp, i32]
+        L.oracle_viterbi.argtypes = [i32, i32, i32, i64, i32, fp, fp, fp, fp, fp, fp, fp, i32]
+        L.oracle_decode.argtypes = [i32, i32, i32, i64, i32, fp, fp, fp, fp, fp]
+        L.oracle_num_threads.argtypes = [i32]
+        for name in ("oracle_codebook", "oracle_bcjr_forward", "oracle_bcjr_backward",
+                     "oracle_viterbi", "oracle_decode", "oracle_num_threads"):
+            getattr(L, name).restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"oracle {what} failed with status {rc}")
+
+
+def num_threads(n: int = 0) -> int:
+    """Set (n > 0) and return the OpenMP thread count used by the C oracle."""
+    return lib().oracle_num_threads(int(n))
+
+
+def codebook(code: int, L: int, lut=None, Q: int = 9) -> np.ndarray:
+    """(2^L, V) float32 codebook: 1MAD / 3INST (V=1) or HYB from a (2^Q, 2) LUT."""
+    V = 2 if code == CODE_HYB else 1
+    out = np.empty((1 << L, V), dtype=np.float32)
+    lut_a = None if lut is None else _f32(lut)
+    _check(lib().oracle_codebook(code, L, _ptr(lut_a), Q, _ptr(out)), "codebook")
+    return out
+
+
+def _temps(T, B):
+    T = np.atleast_1d(np.asarray(T, dtype=np.float32))
+    if T.size == 1:
+        return _f32(T), 0
+    assert T.size == B
+    return _f32(T), 1
+
+
+def bcjr_forward(seq, cb, T, L, KV, nthreads: int = 0):
+    """soft (B,N,V) float32 and logZ (B,) float32, computed in float64."""
+    seq = _f32(seq)
+    cb = _f32(cb)
+    B, N, V = seq.shape
+    Ta, per = _temps(T, B)
+    soft = np.empty_like(seq)
+    logZ = np.empty((B,), dtype=np.float32)
+    _check(lib().oracle_bcjr_forward(L, KV, V, B, N, _ptr(seq), _ptr(Ta), per, _ptr(cb),
+                                      _ptr(soft), _ptr(logZ), nthreads), "forward")
+    return soft, logZ
+
+
+def bcjr_backward(seq, cb, T, L, KV, g_soft, g_logZ=None, nthreads: int = 0):
+    """d seq (B,N,V) for L = sum(g_soft * soft) + sum(g_logZ * logZ)."""
+    seq = _f32(seq)
+    cb = _f32(cb)
+    g = _f32(g_soft)
+    B, N, V = seq.shape
+    Ta, per = _temps(T, B)
+    gz = None if g_logZ is None else _f32(np.broadcast_to(np.asarray(g_logZ, np.float32), (B,)))
+    d = np.empty_like(seq)
+    _check(lib().oracle_bcjr_backward(L, KV, V, B, N, _ptr(seq), _ptr(Ta), per, _ptr(cb), _ptr(g),
+                                       _ptr(gz), _ptr(d), nthreads), "backward")
+    return d
+
+
+def viterbi(seq, cb, L, KV, nthreads: int = 0):
+    """Direct-form float32 Viterbi (src/viterbi/encode.py:250-307), batched.
+
+    seq: (B, N, V).  Returns walk (B,N) int32, bitstream (B,N) int32,
+    start_state (B,) int32, recon (B,N,V) float32, mse (B,) float32.
+    """
+    seq = _f32(seq)
+    cb = _f32(cb)
+    B, N, V = seq.shape
+    walk = np.empty((B, N), dtype=np.int32)
+    bits = np.empty((B, N), dtype=np.int32)
+    start = np.empty((B,), dtype=np.int32)
+    recon = np.empty_like(seq)
+    mse = np.empty((B,), dtype=np.float32)
+    _check(lib().oracle_viterbi(L, KV, V, B, N, _ptr(seq), _ptr(cb), _ptr(walk), _ptr(bits),
+                                 _ptr(start), _ptr(recon), _ptr(mse), nthreads), "viterbi")
+    return walk, bits, start, recon, mse
+
+
+def decode(bitstream, start, cb, L, KV):
+    """Replay walks from (bitstream, start_state); returns walk and recon."""
+    bits = np.ascontiguousarray(bitstream, dtype=np.int32)
+    st = np.ascontiguousarray(start, dtype=np.int32)
+    cb = _f32(cb)
+    B, N = bits.shape
+    V = cb.shape[1]
+    walk = np.empty((B, N), dtype=np.int32)
+    recon = np.empty((B, N, V), dtype=np.float32)
+    _check(lib().oracle_decode(L, KV, V, B, N, _ptr(bits), _ptr(st), _ptr(cb), _ptr(walk),
+                                _ptr(recon)), "decode")
+    return walk, recon
+
+
+# ---------------------------------------------------------------------------
+# Literal restatement of the reference's eager algorithm (float64 numpy)
+# ---------------------------------------------------------------------------
+
+def pred_succ_tables(L, KV):
+    """preds[s,p] = (p << (L-kV)) | (s >> kV); succs[s,c] = ((s << kV) | c) & mask.
+
+    src/bcjr/forward_backward.py:62-86 (k*V passed as one bit count)."""
+    S = 1 << L
+    s = np.arange(S, dtype=np.int64)
+    c = np.arange(1 << KV, dtype=np.int64)
+    preds = (c[None, :] << (L - KV)) | (s >> KV)[:, None]
+    succs = ((s[:, None] << KV) & (S - 1)) | c[None, :]
+    return preds, succs
+
+
+def _lse(x, axis):
+    mx = np.max(x, axis=axis, keepdims=True)
+    mx = np.where(np.isfinite(mx), mx, 0.0)
+    return np.squeeze(mx, axis=axis) + np.log(np.sum(np.exp(x - mx), axis=axis))
+
+
+def naive_forward(seq, cb, T, L, KV, return_internals=False):
+    """Gather-over-predecessors BCJR exactly as forward_backward.py:89-232 (float64).
+
+    Returns soft (B,N,V), logZ (B,) [, P, log_alpha, log_beta (B,N,S)].
+    Memory is O(B*N*S): small trellises only.
+    """
+    seq = np.asarray(seq, dtype=np.float64)
+    cb = np.asarray(cb, dtype=np.float64)
+    B, N, V = seq.shape
+    preds, succs = pred_succ_tables(L, KV)
+    T = np.broadcast_to(np.asarray(T, dtype=np.float64).reshape(-1), (B,))
+    cb_sq = (cb * cb).sum(-1)
+    w_dot = np.einsum("bnv,sv->bns", seq, cb)
+    w_sq = (seq * seq).sum(-1, keepdims=True)
+    ll = -(cb_sq[None, None, :] - 2.0 * w_dot + w_sq) / T[:, None, None]
+    la = np.zeros((B, N, 1 << L))
+    prev = np.zeros((B, 1 << L))
+    for t in range(N):
+        prev = ll[:, t] + _lse(prev[:, preds], axis=-1)
+        la[:, t] = prev
+    lb = np.zeros((B, N, 1 << L))
+    nxt = np.zeros((B, 1 << L))
+    for t in range(N - 2, -1, -1):
+        nxt = _lse(ll[:, t + 1][:, succs] + nxt[:, succs], axis=-1)
+        lb[:, t] = nxt
+    logZ = _lse(la[:, -1], axis=-1)
+    P = np.exp(la + lb - logZ[:, None, None])
+    soft = np.einsum("bns,sv->bnv", P, cb)
+    if return_internals:
+        return soft, logZ, P, la, lb
+    return soft, logZ
+
+
+# ---------------------------------------------------------------------------
+# Brute force (exhaustive path enumeration, float64)
+# ---------------------------------------------------------------------------
+
+def enumerate_paths(L, KV, N):
+    """All valid state paths (s_0..s_{N-1}) of the bitshift trellis, (P, N) int64."""
+    S, R = 1 << L, 1 << KV
+    paths = np.arange(S, dtype=np.int64)[:, None]
+    for _ in range(N - 1):
+        nxt = ((paths[:, -1:] << KV) & (S - 1))[:, :, None] | np.arange(R)[None, None, :]
+        paths = np.concatenate(
+            [np.repeat(paths, R, axis=0), nxt.reshape(-1, 1)], axis=1)
+    return paths
+
+
+def brute_force(seq1, cb, T, L, KV, g=None, g_logZ=0.0):
+    """Exact quantities for ONE sequence (N,V) by enumerating every path.
+
+    The start state s_{-1} is free (2^kV predecessors of s_0 each contribute
+    weight 1), matching log_alpha_{-1} = 0 in forward_backward.py:143.
+    Returns dict with logZ, soft (N,V), marg (N,S), and, when g (N,V) is given,
+    grad (N,V) = (2/T) [Cov(F, c(s_t)) + g_logZ*(E c(s_t) - w_t)], the exact
+    gradient of sum(g*soft) + g_logZ*logZ.  Also min-cost path data.
+    """
+    seq1 = np.asarray(seq1, dtype=np.float64)
+    cb = np.asarray(cb, dtype=np.float64)
+    N, V = seq1.shape
+    paths = enumerate_paths(L, KV, N)
+    cw = cb[paths]                                   # (P, N, V)
+    cost = ((cw - seq1[None]) ** 2).sum(-1)          # (P, N)
+    logw = -cost.sum(1) / T
+    mx = logw.max()
+    wts = np.exp(logw - mx)
+    Zs = wts.sum()
+    logZ = mx + np.log(Zs) + KV * np.log(2.0)
+    pw = wts / Zs
+    soft = np.einsum("p,pnv->nv", pw, cw)
+    marg = np.zeros((N, 1 << L))
+    for t in range(N):
+        np.add.at(marg[t], paths[:, t], pw)
+    out = {"logZ": logZ, "soft": soft, "marg": marg, "paths": paths, "cost": cost.sum(1)}
+    if g is not None:
+        g = np.asarray(g, dtype=np.float64)
+        F = np.einsum("nv,pnv->p", g, cw)
+        EF = (pw * F).sum()
+        cov = np.einsum("p,pnv->nv", pw * (F - EF), cw)
+        out["grad"] = (2.0 / T) * (cov + g_logZ * (soft - seq1))
+    return out
+
+
+def finite_difference_grad(seq1, cb, T, L, KV, g, g_logZ=0.0, h=1e-5):
+    """Central differences of sum(g*soft)+g_logZ*logZ through brute_force (float64)."""
+    seq1 = np.asarray(seq1, dtype=np.float64)
+    grad = np.zeros_like(seq1)
+    for idx in itertools.product(*[range(d) for d in seq1.shape]):
+        vals = []
+        for sgn in (+1, -1):
+            x = seq1.copy()
+            x[idx] += sgn * h
+            r = brute_force(x, cb, T, L, KV)
+            vals.append((np.asarray(g) * r["soft"]).sum() + g_logZ * r["logZ"])
+        grad[idx] = (vals[0] - vals[1]) / (2 * h)
+    return grad
+
+
+# ---------------------------------------------------------------------------
+# Bit packing of per-step indices
+# ---------------------------------------------------------------------------
+
+def pack_bits(bitstream, KV):
+    """Pack (B, N) indices of KV bits each, LSB-first, into (B, ceil(N*KV/8)) uint8.
+
+    Step t occupies bits [t*KV, (t+1)*KV) of the little-endian byte string.
+    Only KV in {1, 2, 4, 8} is supported (indices never straddle a byte).
+    """
+    bits = np.asarray(bitstream, dtype=np.uint32)
+    B, N = bits.shape
+    assert KV in (1, 2, 4, 8)
+    per = 8 // KV
+    nbytes = (N * KV + 7) // 8
+    out = np.zeros((B, nbytes), dtype=np.uint8)
+    for t in range(N):
+        out[:, t // per] |= ((bits[:, t] & ((1 << KV) - 1)) << ((t % per) * KV)).astype(np.uint8)
+    return out
+
+
+def unpack_bits(packed, N, KV):
+    packed = np.asarray(packed, dtype=np.uint8)
+    per = 8 // KV
+    t = np.arange(N)
+    return ((packed[:, t // per] >> ((t % per) * KV)) & ((1 << KV) - 1)).astype(np.int32)

@@ -1,0 +1,19 @@
+"""MI355X-native BCJR forward-backward engine for the trellis-coded quantizer.
+
+Python surface mirroring the reference's src/bcjr package; all compute runs in
+the gfx950 HIP kernels of libbcjr_hip.so (C ABI in include/bcjr_hip.h).
+"""
+from .forward_backward import (  # noqa: F401
+    BcjrFunction, K_BITS, L_BITS, V_DIM, bcjr_forward_backward, bcjr_forward_backward_monolithic,
+    build_pred_succ_tables,
+)
+from .codes import make_1mad_codebook, make_3inst_codebook, make_hyb_codebook_gpu  # noqa: F401
+from .viterbi import (  # noqa: F401
+    viterbi_decode_v_batched, viterbi_encode_chunked, viterbi_encode_v_batched_hip,
+)
+from .quant import (  # noqa: F401
+    bcjr_quantize_tiles, bcjr_quantize_weight_rotated, tile_for_viterbi, untile_from_viterbi,
+)
+from ._lib import LIB_PATH, load as load_library  # noqa: F401
+
+__version__ = "0.1.0"

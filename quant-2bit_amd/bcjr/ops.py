@@ -1,0 +1,203 @@
+"""Tensor-level wrappers over the C ABI: allocate outputs and workspace with
+torch's caching allocator, pass pointers and the current stream, raise on error.
+
+Shapes follow the reference: sequences (B, N, V) float32, codebook (2^L, V),
+bitstreams / walks (B, N) int32, start states (B,) int32.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import CODE_1MAD, CODE_3INST, CODE_HYB, CODE_TABLE, OP_BACKWARD, OP_FORWARD, OP_VITERBI
+
+
+@dataclass(frozen=True)
+class Spec:
+    """Static description of one trellis quantizer (everything but B, N, T)."""
+    L: int
+    k: int
+    V: int
+    code: int = CODE_TABLE
+    Q: int = 9
+
+    @property
+    def kV(self) -> int:
+        return self.k * self.V
+
+    @property
+    def S(self) -> int:
+        return 1 << self.L
+
+    def problem(self, B: int, N: int, t_per_seq: bool = False) -> _lib.Problem:
+        return _lib.Problem(self.L, self.k, self.V, int(B), int(N), self.code, self.Q, int(bool(t_per_seq)))
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _workspace(prob: _lib.Problem, op: int, device: torch.device) -> torch.Tensor:
+    nbytes = ctypes.c_size_t(0)
+    _lib.check(_lib.load().bcjr_workspace_bytes(ctypes.byref(prob), op, ctypes.byref(nbytes)),
+               "bcjr_workspace_bytes")
+    return torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=device)
+
+
+def _temperature(T, B: int, device: torch.device):
+    """float32 device tensor holding one T, or B of them; returns (tensor, per_seq)."""
+    if torch.is_tensor(T):
+        Tt = T.detach().to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    else:
+        Tt = torch.tensor([float(T)], dtype=torch.float32, device=device)
+    if Tt.numel() == 1:
+        return Tt, False
+    if Tt.numel() != B:
+        raise AssertionError(f"T has {Tt.numel()} values; expected 1 or B={B}")
+    return Tt, True
+
+
+def _table(spec: Spec, codebook):
+    """Pointer source for the codeword generator: table, HYB LUT or nothing."""
+    if spec.code == CODE_TABLE:
+        return codebook.detach().to(torch.float32).contiguous()
+    if spec.code == CODE_HYB:
+        return codebook.detach().to(torch.float32).contiguous()  # the (2^Q, 2) LUT
+    return None
+
+
+def forward(spec: Spec, seq: torch.Tensor, T, table: torch.Tensor | None):
+    """soft (B,N,V) float32 and logZ (B,) float32."""
+    with torch.cuda.device(seq.device):
+        seq = seq.detach().to(torch.float32).contiguous()
+        B, N, V = seq.shape
+        Tt, per = _temperature(T, B, seq.device)
+        soft = torch.empty_like(seq)
+        logZ = torch.empty((B,), dtype=torch.float32, device=seq.device)
+        if B == 0:
+            return soft, logZ
+        prob = spec.problem(B, N, per)
+        ws = _workspace(prob, OP_FORWARD, seq.device)
+        _lib.check(_lib.load().bcjr_forward(
+            ctypes.byref(prob), _lib.ptr(seq), _lib.ptr(Tt), _lib.ptr(table), _lib.ptr(soft),
+            _lib.ptr(logZ), _lib.ptr(ws), ws.numel(), _stream(seq.device)), "bcjr_forward")
+        return soft, logZ
+
+
+def forward_internals(spec: Spec, seq: torch.Tensor, T, table: torch.Tensor | None):
+    """soft, logZ, P, log_alpha, log_beta; the last three are (B, N, 2^L) float32."""
+    with torch.cuda.device(seq.device):
+        seq = seq.detach().to(torch.float32).contiguous()
+        B, N, V = seq.shape
+        Tt, per = _temperature(T, B, seq.device)
+        soft = torch.empty_like(seq)
+        logZ = torch.empty((B,), dtype=torch.float32, device=seq.device)
+        P = torch.empty((B, N, spec.S), dtype=torch.float32, device=seq.device)
+        la = torch.empty_like(P)
+        lb = torch.empty_like(P)
+        if B == 0:
+            return soft, logZ, P, la, lb
+        prob = spec.problem(B, N, per)
+        ws = _workspace(prob, OP_FORWARD, seq.device)
+        _lib.check(_lib.load().bcjr_forward_internals(
+            ctypes.byref(prob), _lib.ptr(seq), _lib.ptr(Tt), _lib.ptr(table), _lib.ptr(soft),
+            _lib.ptr(logZ), _lib.ptr(P), _lib.ptr(la), _lib.ptr(lb), _lib.ptr(ws), ws.numel(),
+            _stream(seq.device)), "bcjr_forward_internals")
+        return soft, logZ, P, la, lb
+
+
+def backward(spec: Spec, seq: torch.Tensor, T, table, g_soft, g_logZ=None):
+    """d seq (B,N,V) float32 of sum(g_soft*soft) + sum(g_logZ*logZ)."""
+    with torch.cuda.device(seq.device):
+        seq = seq.detach().to(torch.float32).contiguous()
+        B, N, V = seq.shape
+        Tt, per = _temperature(T, B, seq.device)
+        g = g_soft.detach().to(torch.float32).contiguous() if g_soft is not None else torch.zeros_like(seq)
+        gz = None
+        if g_logZ is not None:
+            gz = g_logZ.detach().to(device=seq.device, dtype=torch.float32).reshape(-1).expand(B).contiguous()
+        d = torch.empty_like(seq)
+        if B == 0:
+            return d
+        prob = spec.problem(B, N, per)
+        ws = _workspace(prob, OP_BACKWARD, seq.device)
+        _lib.check(_lib.load().bcjr_backward(
+            ctypes.byref(prob), _lib.ptr(seq), _lib.ptr(Tt), _lib.ptr(table), None, _lib.ptr(g),
+            _lib.ptr(gz), _lib.ptr(d), _lib.ptr(ws), ws.numel(), _stream(seq.device)), "bcjr_backward")
+        return d
+
+
+def viterbi(spec: Spec, seq: torch.Tensor, table, want_packed: bool = True):
+    """Returns dict: walk, bitstream (B,N) int32; start (B,) int32; recon (B,N,V);
+    mse (B,); packed (B, ceil(N*kV/8)) uint8 (if kV divides 8 and want_packed)."""
+    with torch.cuda.device(seq.device):
+        seq = seq.detach().to(torch.float32).contiguous()
+        B, N, V = seq.shape
+        dev = seq.device
+        out = {
+            "walk": torch.empty((B, N), dtype=torch.int32, device=dev),
+            "bitstream": torch.empty((B, N), dtype=torch.int32, device=dev),
+            "start": torch.empty((B,), dtype=torch.int32, device=dev),
+            "recon": torch.empty_like(seq),
+            "mse": torch.empty((B,), dtype=torch.float32, device=dev),
+        }
+        packed = None
+        if want_packed and 8 % spec.kV == 0:
+            packed = torch.empty((B, (N * spec.kV + 7) // 8), dtype=torch.uint8, device=dev)
+        out["packed"] = packed
+        if B == 0:
+            return out
+        prob = spec.problem(B, N)
+        ws = _workspace(prob, OP_VITERBI, dev)
+        _lib.check(_lib.load().bcjr_viterbi(
+            ctypes.byref(prob), _lib.ptr(seq), _lib.ptr(table), _lib.ptr(out["walk"]),
+            _lib.ptr(out["bitstream"]), _lib.ptr(out["start"]), _lib.ptr(out["recon"]),
+            _lib.ptr(out["mse"]), _lib.ptr(packed), _lib.ptr(ws), ws.numel(), _stream(dev)),
+            "bcjr_viterbi")
+        return out
+
+
+def decode(spec: Spec, start: torch.Tensor, table, bitstream=None, packed=None, N: int | None = None):
+    """Replay walks; returns (walk (B,N) int32, recon (B,N,V) float32)."""
+    dev = start.device
+    with torch.cuda.device(dev):
+        start = start.to(torch.int32).contiguous()
+        B = start.shape[0]
+        if bitstream is not None:
+            bitstream = bitstream.to(torch.int32).contiguous()
+            N = bitstream.shape[1]
+        elif packed is not None:
+            packed = packed.to(torch.uint8).contiguous()
+            if N is None:
+                raise AssertionError("N is required with a packed bitstream")
+        else:
+            raise AssertionError("need bitstream or packed")
+        walk = torch.empty((B, N), dtype=torch.int32, device=dev)
+        recon = torch.empty((B, N, spec.V), dtype=torch.float32, device=dev)
+        if B == 0:
+            return walk, recon
+        prob = spec.problem(B, N)
+        _lib.check(_lib.load().bcjr_decode(
+            ctypes.byref(prob), _lib.ptr(bitstream), _lib.ptr(packed), _lib.ptr(start),
+            _lib.ptr(table), _lib.ptr(walk), _lib.ptr(recon), _stream(dev)), "bcjr_decode")
+        return walk, recon
+
+
+def codebook(code: int, L: int, device, lut: torch.Tensor | None = None, Q: int = 9) -> torch.Tensor:
+    """(2^L, V) float32 codebook from a generator (1MAD, 3INST or HYB)."""
+    device = torch.device(device)
+    V = 2 if code == CODE_HYB else 1
+    out = torch.empty((1 << L, V), dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        lut_t = None if lut is None else lut.detach().to(device=device, dtype=torch.float32).contiguous()
+        prob = _lib.Problem(L, 2, V, 0, 1, code, Q, 0)
+        _lib.check(_lib.load().bcjr_codebook(ctypes.byref(prob), _lib.ptr(lut_t), _lib.ptr(out),
+                                             _stream(device)), "bcjr_codebook")
+    return out
+
+
+__all__ = ["Spec", "forward", "forward_internals", "backward", "viterbi", "decode", "codebook",
+           "CODE_TABLE", "CODE_1MAD", "CODE_3INST", "CODE_HYB"]

@@ -1,0 +1,78 @@
+"""Chunked BCJR quantizer op around the node (src/bcjr/bcjr_quant.py:63-156).
+
+Tiling follows src/qat/ste.py:138-159: an (m, n) matrix becomes
+(n_col_blocks * n_row_blocks) sequences of Tx*Ty weights, block index
+col_block * n_row_blocks + row_block, each 16x16 tile flattened row-major, then
+viewed as (B, N, V) with N = Tx*Ty / V.  The RMS scale is detached
+(bcjr_quant.py:140).  RHT wrapping (bcjr_quantize_weight) is not part of this
+package.
+"""
+from __future__ import annotations
+
+import torch
+
+from .forward_backward import K_BITS, L_BITS, V_DIM, bcjr_forward_backward
+
+TX = 16
+TY = 16
+BCJR_CHUNK = None  # whole batch per launch; workspace memory is bounded by the engine
+
+
+def tile_for_viterbi(W, Tx=TX, Ty=TY):
+    """(m, n) -> (n_col*n_row, Tx*Ty) sequences and (n_row, n_col)  (ste.py:138-149)."""
+    m, n = W.shape
+    if m % Tx or n % Ty:
+        raise AssertionError(f"shape {(m, n)} not tileable by {(Tx, Ty)}")
+    n_row, n_col = m // Tx, n // Ty
+    seqs = W.reshape(m, n_col, Ty).permute(1, 0, 2).contiguous().reshape(n_col * n_row, Tx * Ty)
+    return seqs, (n_row, n_col)
+
+
+def untile_from_viterbi(recons, shape_info, shape_mn, Tx=TX, Ty=TY):
+    """Inverse of tile_for_viterbi (ste.py:152-159)."""
+    n_row, n_col = shape_info
+    m, n = shape_mn
+    return recons.reshape(n_col, m, Ty).permute(1, 0, 2).contiguous().reshape(m, n)
+
+
+def bcjr_quantize_tiles(sequences, codebook, T_temp, preds=None, succs=None,
+                        chunk_size=BCJR_CHUNK, use_checkpoint=True,
+                        L=L_BITS, k=K_BITS, V=V_DIM):
+    """(B, N, V) -> soft (B, N, V), optionally in chunks (bcjr_quant.py:85-122).
+
+    The node keeps only its inputs for backward and recomputes on the GPU, so
+    activation checkpointing would only repeat the forward; use_checkpoint is
+    accepted for signature compatibility and not applied."""
+    B = sequences.shape[0]
+    if chunk_size is None or chunk_size >= B:
+        soft, _ = bcjr_forward_backward(sequences, codebook, T_temp, L=L, k=k, V=V,
+                                        preds=preds, succs=succs)
+        return soft
+    outs = []
+    for i in range(0, B, chunk_size):
+        Ti = T_temp
+        if torch.is_tensor(T_temp) and T_temp.numel() == B:
+            Ti = T_temp[i:i + chunk_size]
+        soft, _ = bcjr_forward_backward(sequences[i:i + chunk_size], codebook, Ti, L=L, k=k, V=V,
+                                        preds=preds, succs=succs)
+        outs.append(soft)
+    return torch.cat(outs, dim=0)
+
+
+def bcjr_quantize_weight_rotated(W_rotated, codebook, T_temp, preds=None, succs=None,
+                                 chunk_size=BCJR_CHUNK, Tx=TX, Ty=TY,
+                                 L=L_BITS, k=K_BITS, V=V_DIM):
+    """Soft-quantize an already-rotated (m, n) weight (bcjr_quant.py:125-156)."""
+    m, n = W_rotated.shape
+    W_scale = W_rotated.detach().pow(2).mean().sqrt().clamp(min=1e-30)
+    W_unit = W_rotated / W_scale
+    seqs_flat, shape_info = tile_for_viterbi(W_unit, Tx, Ty)
+    B, T_seq = seqs_flat.shape
+    seqs = seqs_flat.view(B, T_seq // V, V)
+    soft = bcjr_quantize_tiles(seqs, codebook, T_temp, preds, succs, chunk_size, L=L, k=k, V=V)
+    W_q_unit = untile_from_viterbi(soft.contiguous().view(B, T_seq), shape_info, (m, n), Tx, Ty)
+    return W_q_unit * W_scale
+
+
+__all__ = ["TX", "TY", "tile_for_viterbi", "untile_from_viterbi", "bcjr_quantize_tiles",
+           "bcjr_quantize_weight_rotated"]

@@ -1,0 +1,393 @@
+// C ABI of the engine (include/bcjr_hip.h): validation, launch geometry,
+// workspace sizing and launches on the caller's stream.  No allocation, no host
+// synchronisation, no exceptions across the boundary.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/bcjr_hip.h"
+#include "bcjr_device.h"
+#include "bcjr_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(BCJR_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+struct DeviceInfo {
+  bool valid = false;
+  int num_cu = 0;
+  size_t max_lds = 0;
+};
+
+std::mutex g_dev_mu;
+DeviceInfo g_dev[64];
+
+int device_info(DeviceInfo* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= 64) return fail(BCJR_EHIP, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  if (!g_dev[dev].valid) {
+    int cu = 0, lds = 0;
+    e = hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
+    e = hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MaxSharedMemoryPerBlock)");
+    g_dev[dev].num_cu = cu;
+    g_dev[dev].max_lds = (size_t)lds;
+    g_dev[dev].valid = true;
+  }
+  *out = g_dev[dev];
+  return BCJR_OK;
+}
+
+// Launch geometry of one operation for one problem.
+struct Plan {
+  int KV = 0, R = 0, NSUB = 0;
+  int NT = 0, NB = 0, NU = 0;
+  int nthr = 0, upt = 0;
+  bool cache = false;
+  const void* fn = nullptr;
+  size_t lds = 0;
+  size_t slot_bytes = 0;
+  int max_blocks = 0;  // resident blocks on the device
+};
+
+int validate(const bcjr_problem* p) {
+  if (!p) return fail(BCJR_EINVAL, "problem is NULL");
+  if (p->V != 1 && p->V != 2) return fail(BCJR_EINVAL, "V=%d must be 1 or 2", p->V);
+  if (p->k < 1) return fail(BCJR_EINVAL, "k=%d must be >= 1", p->k);
+  const int KV = p->k * p->V;
+  if (KV != 1 && KV != 2 && KV != 4)
+    return fail(BCJR_EUNSUPPORTED, "k*V=%d: only 1, 2 or 4 bits per step are built", KV);
+  if (p->L < 2 * KV || p->L > 16)
+    return fail(BCJR_EUNSUPPORTED, "L=%d outside [%d, 16] for k*V=%d", p->L, 2 * KV, KV);
+  if (KV == 1 && p->L > 11) return fail(BCJR_EUNSUPPORTED, "k*V=1 supports L <= 11 (got %d)", p->L);
+  if (p->B < 0) return fail(BCJR_EINVAL, "B=%lld must be >= 0", (long long)p->B);
+  if (p->N < 1 || p->N > 4096) return fail(BCJR_EINVAL, "N=%lld outside [1, 4096]", (long long)p->N);
+  switch (p->code) {
+    case BCJR_CODE_TABLE: break;
+    case BCJR_CODE_1MAD:
+    case BCJR_CODE_3INST:
+      if (p->V != 1) return fail(BCJR_EINVAL, "1MAD/3INST codes are scalar (V=1), got V=%d", p->V);
+      break;
+    case BCJR_CODE_HYB:
+      if (p->V != 2) return fail(BCJR_EINVAL, "HYB code is 2-D (V=2), got V=%d", p->V);
+      if (p->Q < 1 || p->Q > 12 || p->Q > 15) return fail(BCJR_EINVAL, "HYB Q=%d outside [1, 12]", p->Q);
+      break;
+    default: return fail(BCJR_EINVAL, "unknown code %d", p->code);
+  }
+  return BCJR_OK;
+}
+
+enum { OP_FWD = BCJR_OP_FORWARD, OP_BWD = BCJR_OP_BACKWARD, OP_VIT = BCJR_OP_VITERBI };
+
+// Plans depend on (device, op, L, k, V, N, code, Q) only; they are cached so that
+// steady-state calls (and calls made while a stream is being captured into a
+// graph) do no attribute or occupancy queries.
+struct PlanKey {
+  int dev, op, L, k, V, code, Q;
+  long long N;
+  bool operator==(const PlanKey& o) const {
+    return dev == o.dev && op == o.op && L == o.L && k == o.k && V == o.V && code == o.code &&
+           Q == o.Q && N == o.N;
+  }
+};
+constexpr int kPlanCache = 64;
+std::mutex g_plan_mu;
+PlanKey g_plan_keys[kPlanCache];
+Plan g_plans[kPlanCache];
+int g_plan_count = 0, g_plan_next = 0;
+
+int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan* pl);
+
+int make_plan(const bcjr_problem* p, int op, Plan* pl) {
+  int rc = validate(p);
+  if (rc) return rc;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  const PlanKey key = {dev, op, p->L, p->k, p->V, p->code, p->code == BCJR_CODE_HYB ? p->Q : 0,
+                       (long long)p->N};
+  {
+    std::lock_guard<std::mutex> lk(g_plan_mu);
+    for (int i = 0; i < g_plan_count; ++i)
+      if (g_plan_keys[i] == key) {
+        *pl = g_plans[i];
+        return BCJR_OK;
+      }
+  }
+  DeviceInfo di;
+  rc = device_info(&di);
+  if (rc) return rc;
+  rc = make_plan_uncached(p, op, di, pl);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  const int slot = g_plan_count < kPlanCache ? g_plan_count++ : (g_plan_next++ % kPlanCache);
+  g_plan_keys[slot] = key;
+  g_plans[slot] = *pl;
+  return BCJR_OK;
+}
+
+int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan* pl) {
+  const int KV = p->k * p->V, R = 1 << KV, RO = R < 4 ? R : 4;
+  pl->KV = KV;
+  pl->R = R;
+  pl->NSUB = R / RO;
+  pl->NT = 1 << (p->L - KV);
+  pl->NB = pl->NT >> KV;
+  pl->NU = pl->NB * pl->NSUB;
+  const int max_thr = 512;
+  int nthr = ((pl->NU + 63) / 64) * 64;
+  nthr = std::min(nthr, max_thr);
+  const int upt = (pl->NU + nthr - 1) / nthr;
+  if (upt != 1 && upt != 2 && upt != 4 && upt != 8)
+    return fail(BCJR_EUNSUPPORTED, "no launch shape for L=%d k*V=%d (units/thread %d)", p->L, KV, upt);
+  pl->nthr = nthr;
+  pl->upt = upt;
+  const int nwaves = nthr / 64;
+  const int N = (int)p->N;
+  if (op == OP_FWD || op == OP_VIT) {
+    pl->cache = (pl->NSUB == 1) && (upt * R * R * p->V <= 128);
+    pl->fn = (op == OP_FWD) ? bcjr::fwd_kernel_ptr(KV, p->V, p->code, upt, pl->cache)
+                            : bcjr::vit_kernel_ptr(KV, p->V, p->code, upt, pl->cache);
+    pl->lds = (op == OP_FWD) ? bcjr::fwd_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q)
+                             : bcjr::vit_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q);
+    pl->slot_bytes = (op == OP_FWD) ? (size_t)N * pl->NT * sizeof(float) : (size_t)N * pl->NT;
+  } else {
+    pl->cache = false;
+    pl->fn = bcjr::bwd_kernel_ptr(KV, p->V, p->code, upt);
+    pl->lds = bcjr::bwd_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q);
+    pl->slot_bytes = (size_t)N * 2 * pl->NT * sizeof(float);
+  }
+  pl->slot_bytes = (pl->slot_bytes + 255) & ~(size_t)255;
+  if (!pl->fn)
+    return fail(BCJR_EUNSUPPORTED, "no kernel built for L=%d k=%d V=%d code=%d (units/thread %d)",
+                p->L, p->k, p->V, p->code, upt);
+  if (pl->lds > di.max_lds)
+    return fail(BCJR_EUNSUPPORTED, "needs %zu bytes of LDS per workgroup (device limit %zu); reduce N=%lld",
+                pl->lds, di.max_lds, (long long)p->N);
+  hipError_t e = hipFuncSetAttribute(pl->fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl->lds);
+  if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
+  int per_cu = 0;
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, pl->fn, nthr, pl->lds);
+  if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+  if (per_cu < 1) return fail(BCJR_EUNSUPPORTED, "kernel cannot be resident (%d threads, %zu B LDS)", nthr, pl->lds);
+  pl->max_blocks = per_cu * di.num_cu;
+  return BCJR_OK;
+}
+
+int launch(const Plan& pl, long long B, size_t ws_bytes, void* params, hipStream_t stream) {
+  if (B == 0) return BCJR_OK;
+  long long slots = (long long)(ws_bytes / pl.slot_bytes);
+  if (slots < 1)
+    return fail(BCJR_EWORKSPACE, "workspace of %zu bytes is smaller than one sequence slot (%zu bytes)",
+                ws_bytes, pl.slot_bytes);
+  const long long grid = std::min<long long>(std::min<long long>(B, pl.max_blocks), slots);
+  void* args[] = {params};
+  hipError_t e = hipLaunchKernel(pl.fn, dim3((unsigned)grid), dim3((unsigned)pl.nthr), args, pl.lds, stream);
+  if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel");
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  return BCJR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bcjr_workspace_bytes(const bcjr_problem* prob, int op, size_t* bytes) {
+  if (!bytes) return fail(BCJR_EINVAL, "bytes is NULL");
+  if (op != OP_FWD && op != OP_BWD && op != OP_VIT) return fail(BCJR_EINVAL, "unknown op %d", op);
+  Plan pl;
+  int rc = make_plan(prob, op, &pl);
+  if (rc) return rc;
+  const long long slots = std::max<long long>(1, std::min<long long>(prob->B, pl.max_blocks));
+  *bytes = (size_t)slots * pl.slot_bytes;
+  return BCJR_OK;
+}
+
+int bcjr_forward(const bcjr_problem* prob, const float* seq, const float* T, const float* codebook_or_lut,
+                 float* soft, float* logZ, void* ws, size_t ws_bytes, hipStream_t stream) {
+  Plan pl;
+  int rc = make_plan(prob, OP_FWD, &pl);
+  if (rc) return rc;
+  if (prob->B == 0) return BCJR_OK;
+  if (!seq || !T || !soft || !ws) return fail(BCJR_EINVAL, "seq, T, soft and ws must be non-NULL");
+  if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
+    return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  bcjr::FwdParams P = {};
+  P.seq = seq;
+  P.T = T;
+  P.table = codebook_or_lut;
+  P.soft = soft;
+  P.logZ = logZ;
+  P.ws = static_cast<float*>(ws);
+  P.B = prob->B;
+  P.N = (int)prob->N;
+  P.L = prob->L;
+  P.Q = prob->Q;
+  P.t_per_seq = prob->t_per_seq ? 1 : 0;
+  return launch(pl, prob->B, ws_bytes, &P, stream);
+}
+
+int bcjr_forward_internals(const bcjr_problem* prob, const float* seq, const float* T,
+                           const float* codebook_or_lut, float* soft, float* logZ, float* marginals,
+                           float* log_alpha, float* log_beta, void* ws, size_t ws_bytes, hipStream_t stream) {
+  Plan pl;
+  int rc = make_plan(prob, OP_FWD, &pl);
+  if (rc) return rc;
+  if (prob->B == 0) return BCJR_OK;
+  if (!seq || !T || !soft || !ws || !marginals || !log_alpha || !log_beta)
+    return fail(BCJR_EINVAL, "seq, T, soft, ws, marginals, log_alpha and log_beta must be non-NULL");
+  if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
+    return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  bcjr::FwdParams P = {};
+  P.seq = seq;
+  P.T = T;
+  P.table = codebook_or_lut;
+  P.soft = soft;
+  P.logZ = logZ;
+  P.ws = static_cast<float*>(ws);
+  P.P_out = marginals;
+  P.la_out = log_alpha;
+  P.lb_out = log_beta;
+  P.B = prob->B;
+  P.N = (int)prob->N;
+  P.L = prob->L;
+  P.Q = prob->Q;
+  P.t_per_seq = prob->t_per_seq ? 1 : 0;
+  return launch(pl, prob->B, ws_bytes, &P, stream);
+}
+
+int bcjr_backward(const bcjr_problem* prob, const float* seq, const float* T, const float* codebook_or_lut,
+                  const float* logZ, const float* g_soft, const float* g_logZ, float* g_seq, void* ws,
+                  size_t ws_bytes, hipStream_t stream) {
+  (void)logZ;
+  Plan pl;
+  int rc = make_plan(prob, OP_BWD, &pl);
+  if (rc) return rc;
+  if (prob->B == 0) return BCJR_OK;
+  if (!seq || !T || !g_soft || !g_seq || !ws)
+    return fail(BCJR_EINVAL, "seq, T, g_soft, g_seq and ws must be non-NULL");
+  if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
+    return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  bcjr::BwdParams P = {};
+  P.seq = seq;
+  P.T = T;
+  P.table = codebook_or_lut;
+  P.g_soft = g_soft;
+  P.g_logZ = g_logZ;
+  P.g_seq = g_seq;
+  P.ws = static_cast<float*>(ws);
+  P.B = prob->B;
+  P.N = (int)prob->N;
+  P.L = prob->L;
+  P.Q = prob->Q;
+  P.t_per_seq = prob->t_per_seq ? 1 : 0;
+  return launch(pl, prob->B, ws_bytes, &P, stream);
+}
+
+int bcjr_viterbi(const bcjr_problem* prob, const float* seq, const float* codebook_or_lut, int32_t* walk,
+                 int32_t* bitstream, int32_t* start_state, float* recon, float* mse, uint8_t* packed, void* ws,
+                 size_t ws_bytes, hipStream_t stream) {
+  Plan pl;
+  int rc = make_plan(prob, OP_VIT, &pl);
+  if (rc) return rc;
+  if (prob->B == 0) return BCJR_OK;
+  if (!seq || !ws) return fail(BCJR_EINVAL, "seq and ws must be non-NULL");
+  if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
+    return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  if (packed && 8 % pl.KV != 0) return fail(BCJR_EINVAL, "packing needs k*V to divide 8");
+  bcjr::VitParams P = {};
+  P.seq = seq;
+  P.table = codebook_or_lut;
+  P.walk = walk;
+  P.bits = bitstream;
+  P.start = start_state;
+  P.recon = recon;
+  P.mse = mse;
+  P.packed = packed;
+  P.ws = static_cast<uint8_t*>(ws);
+  P.B = prob->B;
+  P.N = (int)prob->N;
+  P.L = prob->L;
+  P.Q = prob->Q;
+  return launch(pl, prob->B, ws_bytes, &P, stream);
+}
+
+int bcjr_decode(const bcjr_problem* prob, const int32_t* bitstream, const uint8_t* packed,
+                const int32_t* start_state, const float* codebook_or_lut, int32_t* walk, float* recon,
+                hipStream_t stream) {
+  int rc = validate(prob);
+  if (rc) return rc;
+  if (prob->B == 0) return BCJR_OK;
+  if ((!bitstream && !packed) || !start_state)
+    return fail(BCJR_EINVAL, "need start_state and one of bitstream / packed");
+  if (recon && prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
+    return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  const int KV = prob->k * prob->V;
+  const void* fn = bcjr::decode_kernel_ptr(KV, prob->V, prob->code);
+  if (!fn) return fail(BCJR_EUNSUPPORTED, "no decode kernel for k*V=%d V=%d code=%d", KV, prob->V, prob->code);
+  bcjr::DecParams P = {bitstream, packed, start_state, codebook_or_lut, walk, recon,
+                       prob->B, (int)prob->N, prob->L, prob->Q};
+  void* args[] = {&P};
+  const unsigned grid = (unsigned)((prob->B + 255) / 256);
+  hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, stream);
+  if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel(decode)");
+  return BCJR_OK;
+}
+
+int bcjr_codebook(const bcjr_problem* prob, const float* lut, float* codebook_out, hipStream_t stream) {
+  if (!prob) return fail(BCJR_EINVAL, "problem is NULL");
+  if (prob->L < 1 || prob->L > 24) return fail(BCJR_EINVAL, "L=%d outside [1, 24]", prob->L);
+  if (!codebook_out) return fail(BCJR_EINVAL, "codebook_out is NULL");
+  const void* fn = bcjr::codebook_kernel_ptr(prob->code);
+  if (!fn) return fail(BCJR_EINVAL, "code %d has no generator", prob->code);
+  if (prob->code == BCJR_CODE_HYB && (!lut || prob->Q < 1 || prob->Q > 12))
+    return fail(BCJR_EINVAL, "HYB needs a LUT and Q in [1, 12]");
+  bcjr::CbParams P = {lut, codebook_out, 1ll << prob->L, prob->Q};
+  void* args[] = {&P};
+  const unsigned grid = (unsigned)((P.S + 255) / 256);
+  hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, stream);
+  if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel(codebook)");
+  return BCJR_OK;
+}
+
+const char* bcjr_strerror(int status) {
+  switch (status) {
+    case BCJR_OK: return "ok";
+    case BCJR_EINVAL: return "invalid argument";
+    case BCJR_EUNSUPPORTED: return "unsupported configuration";
+    case BCJR_EWORKSPACE: return "workspace too small";
+    case BCJR_EHIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+const char* bcjr_last_error(void) { return g_last_error.c_str(); }
+
+const char* bcjr_version(void) { return "bcjr_hip 0.1.0 (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,47 @@
+// Host-side view of the kernel instances: each kernel translation unit exposes a
+// lookup from (kV, V, code, units-per-thread[, cache]) to the template instance,
+// plus the LDS footprint its launch needs.  The C ABI (bcjr_capi.hip) owns
+// validation, occupancy and launch.
+#pragma once
+
+#include <stddef.h>
+
+namespace bcjr {
+
+struct FwdParams;
+struct BwdParams;
+struct VitParams;
+
+const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool cache);
+const void* bwd_kernel_ptr(int KV, int V, int code, int upt);
+const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache);
+const void* decode_kernel_ptr(int KV, int V, int code);
+const void* codebook_kernel_ptr(int code);
+
+// LDS bytes for one workgroup.
+inline size_t fwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {
+  const size_t NT = (size_t)1 << (L - KV);
+  size_t b = 8u * (size_t)N;                       // C_t (double)
+  b += 4u * (2 * NT + 3 * 16 + (size_t)N * V + (size_t)N * nwaves * V);
+  if (code == 3) b += 4u * ((size_t)2 << Q);
+  return b;
+}
+
+inline size_t bwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {
+  const size_t NT = (size_t)1 << (L - KV);
+  size_t b = 8u * (size_t)N;
+  b += 4u * (2 * NT + 4 * 16 + 2 * (size_t)N * V + (size_t)N * nwaves * (V + 1));
+  if (code == 3) b += 4u * ((size_t)2 << Q);
+  return b;
+}
+
+inline size_t vit_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {
+  const size_t NT = (size_t)1 << (L - KV);
+  (void)nwaves;
+  size_t b = 8u * 16;                                           // per-wave MSE partials
+  b += 4u * (2 * NT + (size_t)N * V + 2 * 16 + (size_t)N);      // state, seq, argmin, walk
+  if (code == 3) b += 4u * ((size_t)2 << Q);
+  return b;
+}
+
+}  // namespace bcjr

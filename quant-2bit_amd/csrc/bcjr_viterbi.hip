@@ -1,0 +1,365 @@
+// T -> 0 mode of the node: min-sum Viterbi on the bitshift trellis, traceback,
+// reconstruction, MSE and kV-bit packing, plus walk replay and codebook fill.
+//
+// Replaces viterbi_encode_v_batched_cuda (src/viterbi/cuda_kernel.py:166-220) and
+// follows the semantics of the numpy encoder viterbi_encode_v
+// (src/viterbi/encode.py:250-307), which fixes the float32 rounding and tie rules:
+//   cum_0 = 0;  cum_t(s) = fl( min_p cum_{t-1}(p*NT + (s >> kV)) + E_t(s) ),
+//   E_t(s)  = fl( sum_v fl( fl(c_v(s) - w_t[v])^2 ) )     (no FMA contraction),
+//   the lowest p wins a tie, the lowest final state wins a tie,
+//   walk_{t-1} = bp_t(walk_t >> kV) * NT + (walk_t >> kV),
+//   start = bp_0(walk_0 >> kV) * NT + (walk_0 >> kV) = walk_0 >> kV,
+//   bitstream_t = walk_t & (2^kV - 1), recon_t = c(walk_t).
+// Min-sum has no transcendentals; the butterfly layout and the per-step LDS
+// exchange are those of the soft kernels.  Backpointers (one byte per reduced
+// state and step) go to the caller's workspace and are staged back through LDS,
+// eight rows at a time, for the traceback.
+#pragma clang fp contract(off)
+
+#include "bcjr_device.h"
+#include "bcjr_kernels.h"
+
+namespace bcjr {
+
+// Strict (value, index) order: smaller value first, then lower index.
+__device__ __forceinline__ bool vi_less(float a, int ia, float b, int ib) {
+  return (a < b) || (a == b && ia < ib);
+}
+
+template <int KV, int V, int CODE, int UPT, bool CACHE>
+__global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
+  constexpr int R = 1 << KV;
+  constexpr int RO = R < 4 ? R : 4;
+  constexpr int NSUB = R / RO;
+  static_assert(!CACHE || NSUB == 1, "codeword cache needs whole butterflies per thread");
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int L = P.L, N = P.N;
+  const int NT = 1 << (L - KV);
+  const int NB = NT >> KV;
+  const int NU = NB * NSUB;
+  const int lgNB = L - 2 * KV;
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
+
+  double* redd = reinterpret_cast<double*>(smem);             // kMaxWaves
+  float* rbuf = reinterpret_cast<float*>(redd + kMaxWaves);    // 2*NT (also traceback staging)
+  float* wbuf = rbuf + 2 * NT;                                 // N*V
+  float* redv = wbuf + N * V;                                  // kMaxWaves
+  int* redi = reinterpret_cast<int*>(redv + kMaxWaves);        // kMaxWaves
+  int* walkbuf = redi + kMaxWaves;                             // N
+  float* lut = reinterpret_cast<float*>(walkbuf + N);
+
+  if constexpr (CODE == CODE_HYB) {
+    const int nl = 2 << P.Q;
+    for (int i = tid; i < nl; i += nthr) lut[i] = P.table[i];
+    __syncthreads();
+  }
+
+  float cw[CACHE ? UPT : 1][CACHE ? R : 1][CACHE ? R : 1][V];
+  if constexpr (CACHE) {
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int u = min(tid + i * nthr, NU - 1);
+#pragma unroll
+      for (int p = 0; p < R; ++p)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          codeword<CODE, V, true>((uint32_t)(p * NT + R * u + r), P.table, lut, P.Q, cw[i][p][r]);
+    }
+  }
+
+  for (long long b = blockIdx.x; b < P.B; b += gridDim.x) {
+    uint8_t* bp = P.ws + (size_t)blockIdx.x * (size_t)N * (size_t)NT;
+    const float* seqb = P.seq + (size_t)b * N * V;
+    for (int i = tid; i < N * V; i += nthr) wbuf[i] = seqb[i];
+    __syncthreads();
+
+    for (int t = 0; t < N; ++t) {
+      const float* prev = rbuf + ((t + 1) & 1) * NT;
+      float* cur = rbuf + (t & 1) * NT;
+      float w[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) w[v] = wbuf[t * V + v];
+#pragma unroll
+      for (int i = 0; i < UPT; ++i) {
+        const int q = tid + i * nthr;
+        __builtin_amdgcn_sched_barrier(0);
+        if (q < NU) {
+          const int u = (CACHE ? q : opaque(q)) & (NB - 1);
+          const int sub = q >> lgNB;
+          float ri[R];
+#pragma unroll
+          for (int p = 0; p < R; ++p) ri[p] = t ? prev[p * NB + u] : 0.0f;
+          float ro[RO];
+          uint32_t bpw = 0;
+#pragma unroll
+          for (int r = 0; r < RO; ++r) {
+            const int rr = sub * RO + r;
+            float best = 0.0f;
+            int bi = 0;
+#pragma unroll
+            for (int p = 0; p < R; ++p) {
+              float c[V];
+              if constexpr (CACHE) {
+#pragma unroll
+                for (int v = 0; v < V; ++v) c[v] = cw[i][p][r][v];
+              } else {
+                codeword<CODE, V, true>((uint32_t)(p * NT + R * u + rr), P.table, lut, P.Q, c);
+              }
+              float e = 0.0f;
+#pragma unroll
+              for (int v = 0; v < V; ++v) {
+                const float d = c[v] - w[v];
+                const float d2 = d * d;
+                e = e + d2;
+              }
+              const float cum = ri[p] + e;
+              if (p == 0 || cum < best) {
+                best = cum;
+                bi = p;
+              }
+            }
+            ro[r] = best;
+            bpw |= (uint32_t)bi << (8 * r);
+          }
+          float* o = cur + R * u + sub * RO;
+#pragma unroll
+          for (int r = 0; r < RO; ++r) o[r] = ro[r];
+          uint8_t* bdst = bp + (size_t)t * NT + R * u + sub * RO;
+#pragma unroll
+          for (int r = 0; r < RO; ++r) bdst[r] = (uint8_t)(bpw >> (8 * r));
+        }
+      }
+      __syncthreads();
+    }
+
+    // Final state: lowest index among the minimal cum_{N-1}(s), recomputed from
+    // min_p cum_{N-2} (still in LDS) in a separate pass over all states.
+    float fbest = INFINITY;
+    int fstate = 0x7fffffff;
+    {
+      const float* prev = rbuf + (N & 1) * NT;  // written at step N-2
+      float w[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) w[v] = wbuf[(N - 1) * V + v];
+      {
+        for (int s = tid; s < (NT << KV); s += nthr) {
+          float c[V];
+          codeword<CODE, V, true>((uint32_t)s, P.table, lut, P.Q, c);
+          float e = 0.0f;
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const float d = c[v] - w[v];
+            const float d2 = d * d;
+            e = e + d2;
+          }
+          const float cum = (N > 1 ? prev[s >> KV] : 0.0f) + e;
+          if (vi_less(cum, s, fbest, fstate)) {
+            fbest = cum;
+            fstate = s;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(fbest, o, 64);
+      const int oi = __shfl_xor(fstate, o, 64);
+      if (vi_less(ov, oi, fbest, fstate)) {
+        fbest = ov;
+        fstate = oi;
+      }
+    }
+    if (lane == 0) {
+      redv[wave] = fbest;
+      redi[wave] = fstate;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float bv = redv[0];
+      int bs = redi[0];
+      for (int w = 1; w < nwaves; ++w)
+        if (vi_less(redv[w], redi[w], bv, bs)) {
+          bv = redv[w];
+          bs = redi[w];
+        }
+      // Only a NaN input leaves no candidate; fall back to state 0 so the
+      // traceback below always indexes inside the trellis.
+      walkbuf[N - 1] = (bs >= 0 && bs < (NT << KV)) ? bs : 0;
+    }
+    __syncthreads();
+
+    // Traceback: stage up to 8 backpointer rows in LDS, walk them on one thread.
+    const int cap = (int)((2 * (size_t)NT * sizeof(float)) / (size_t)NT);
+    uint8_t* stage = reinterpret_cast<uint8_t*>(rbuf);
+    int s = walkbuf[N - 1];
+    for (int hi = N - 1; hi >= 1; hi -= cap) {
+      const int lo = max(1, hi - cap + 1);
+      const int nbytes_rows = (hi - lo + 1) * NT;
+      if ((NT & 3) == 0) {
+        const uint32_t* srcw = reinterpret_cast<const uint32_t*>(bp + (size_t)lo * NT);
+        uint32_t* dstw = reinterpret_cast<uint32_t*>(stage);
+        for (int i = tid; i < (nbytes_rows >> 2); i += nthr) dstw[i] = srcw[i];
+      } else {
+        for (int i = tid; i < nbytes_rows; i += nthr) stage[i] = bp[(size_t)lo * NT + i];
+      }
+      __syncthreads();
+      if (tid == 0) {
+        for (int t = hi; t >= lo; --t) {
+          const int j = s >> KV;
+          s = (int)stage[(size_t)(t - lo) * NT + j] * NT + j;
+          walkbuf[t - 1] = s;
+        }
+      }
+      __syncthreads();
+    }
+
+    // Outputs.
+    double se = 0.0;
+    for (int t = tid; t < N; t += nthr) {
+      const int st = walkbuf[t];
+      if (P.walk) P.walk[(size_t)b * N + t] = st;
+      if (P.bits) P.bits[(size_t)b * N + t] = st & (R - 1);
+      float c[V];
+      codeword<CODE, V, true>((uint32_t)st, P.table, lut, P.Q, c);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if (P.recon) P.recon[((size_t)b * N + t) * V + v] = c[v];
+        const double d = (double)c[v] - (double)wbuf[t * V + v];
+        se += d * d;
+      }
+    }
+    if (P.start && tid == 0) P.start[b] = walkbuf[0] >> KV;
+    if (P.packed) {
+      constexpr int per = 8 / KV;
+      const int nbytes = (N * KV + 7) / 8;
+      for (int i = tid; i < nbytes; i += nthr) {
+        uint32_t byte = 0;
+#pragma unroll
+        for (int qq = 0; qq < per; ++qq) {
+          const int t = i * per + qq;
+          if (t < N) byte |= ((uint32_t)walkbuf[t] & (R - 1)) << (qq * KV);
+        }
+        P.packed[(size_t)b * nbytes + i] = (uint8_t)byte;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) se += __shfl_xor(se, o, 64);
+    if (lane == 0) redd[wave] = se;
+    __syncthreads();
+    if (tid == 0 && P.mse) {
+      double tot = 0.0;
+      for (int w = 0; w < nwaves; ++w) tot += redd[w];
+      P.mse[b] = (float)(tot / (double)(N * V));
+    }
+    __syncthreads();
+  }
+}
+
+// Walk replay: one thread per sequence.
+template <int KV, int V, int CODE>
+__global__ __launch_bounds__(256) void bcjr_decode_kernel(DecParams P) {
+  const long long b = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= P.B) return;
+  constexpr int R = 1 << KV;
+  const uint32_t mask = (P.L >= 32) ? 0xFFFFFFFFu : ((1u << P.L) - 1u);
+  const int nbytes = (P.N * KV + 7) / 8;
+  uint32_t s = (uint32_t)P.start[b];
+  for (int t = 0; t < P.N; ++t) {
+    uint32_t bits;
+    if (P.packed) {
+      constexpr int per = 8 / KV;
+      bits = ((uint32_t)P.packed[(size_t)b * nbytes + t / per] >> ((t % per) * KV)) & (R - 1);
+    } else {
+      bits = (uint32_t)P.bits[(size_t)b * P.N + t] & (R - 1);
+    }
+    s = ((s << KV) | bits) & mask;
+    if (P.walk) P.walk[(size_t)b * P.N + t] = (int32_t)s;
+    if (P.recon) {
+      float c[V];
+      codeword<CODE, V, true>(s, P.table, P.table, P.Q, c);
+#pragma unroll
+      for (int v = 0; v < V; ++v) P.recon[((size_t)b * P.N + t) * V + v] = c[v];
+    }
+  }
+}
+
+// Codebook fill: one thread per state.
+template <int CODE>
+__global__ __launch_bounds__(256) void bcjr_codebook_kernel(CbParams P) {
+  const long long s = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= P.S) return;
+  if constexpr (CODE == CODE_HYB) {
+    float c[2];
+    codeword<CODE_HYB, 2, true>((uint32_t)s, nullptr, P.lut, P.Q, c);
+    P.out[2 * s] = c[0];
+    P.out[2 * s + 1] = c[1];
+  } else {
+    float c[1];
+    codeword<CODE, 1, true>((uint32_t)s, nullptr, nullptr, P.Q, c);
+    P.out[s] = c[0];
+  }
+}
+
+#define BCJR_VIT_CASE(KV_, V_, CODE_, UPT_, CACHE_)                                         \
+  if (KV == KV_ && V == V_ && code == CODE_ && upt == UPT_ && cache == CACHE_)              \
+    return reinterpret_cast<const void*>(&bcjr_viterbi_kernel<KV_, V_, CODE_, UPT_, CACHE_>);
+
+#define BCJR_VIT_UPTS(KV_, V_, CODE_, CACHE_) \
+  BCJR_VIT_CASE(KV_, V_, CODE_, 1, CACHE_)    \
+  BCJR_VIT_CASE(KV_, V_, CODE_, 2, CACHE_)    \
+  BCJR_VIT_CASE(KV_, V_, CODE_, 4, CACHE_)    \
+  BCJR_VIT_CASE(KV_, V_, CODE_, 8, CACHE_)
+
+const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache) {
+  BCJR_VIT_CASE(1, 1, CODE_TABLE, 1, true)
+  BCJR_VIT_UPTS(2, 1, CODE_TABLE, true)
+  BCJR_VIT_UPTS(2, 1, CODE_1MAD, true)
+  BCJR_VIT_UPTS(2, 1, CODE_3INST, true)
+  BCJR_VIT_CASE(2, 2, CODE_TABLE, 1, true)
+  BCJR_VIT_CASE(2, 2, CODE_TABLE, 2, true)
+  BCJR_VIT_CASE(2, 2, CODE_TABLE, 4, true)
+  BCJR_VIT_CASE(2, 2, CODE_HYB, 1, true)
+  BCJR_VIT_CASE(2, 2, CODE_HYB, 2, true)
+  BCJR_VIT_CASE(2, 2, CODE_HYB, 4, true)
+  BCJR_VIT_CASE(4, 1, CODE_TABLE, 1, false)
+  BCJR_VIT_CASE(4, 1, CODE_TABLE, 2, false)
+  BCJR_VIT_CASE(4, 1, CODE_1MAD, 1, false)
+  BCJR_VIT_CASE(4, 1, CODE_1MAD, 2, false)
+  BCJR_VIT_CASE(4, 1, CODE_3INST, 1, false)
+  BCJR_VIT_CASE(4, 1, CODE_3INST, 2, false)
+  BCJR_VIT_CASE(4, 2, CODE_TABLE, 1, false)
+  BCJR_VIT_CASE(4, 2, CODE_TABLE, 2, false)
+  BCJR_VIT_CASE(4, 2, CODE_HYB, 1, false)
+  BCJR_VIT_CASE(4, 2, CODE_HYB, 2, false)
+  return nullptr;
+}
+
+#define BCJR_DEC_CASE(KV_, V_, CODE_) \
+  if (KV == KV_ && V == V_ && code == CODE_) \
+    return reinterpret_cast<const void*>(&bcjr_decode_kernel<KV_, V_, CODE_>);
+
+const void* decode_kernel_ptr(int KV, int V, int code) {
+  BCJR_DEC_CASE(1, 1, CODE_TABLE)
+  BCJR_DEC_CASE(2, 1, CODE_TABLE)
+  BCJR_DEC_CASE(2, 1, CODE_1MAD)
+  BCJR_DEC_CASE(2, 1, CODE_3INST)
+  BCJR_DEC_CASE(2, 2, CODE_TABLE)
+  BCJR_DEC_CASE(2, 2, CODE_HYB)
+  BCJR_DEC_CASE(4, 1, CODE_TABLE)
+  BCJR_DEC_CASE(4, 1, CODE_1MAD)
+  BCJR_DEC_CASE(4, 1, CODE_3INST)
+  BCJR_DEC_CASE(4, 2, CODE_TABLE)
+  BCJR_DEC_CASE(4, 2, CODE_HYB)
+  return nullptr;
+}
+
+const void* codebook_kernel_ptr(int code) {
+  if (code == CODE_1MAD) return reinterpret_cast<const void*>(&bcjr_codebook_kernel<CODE_1MAD>);
+  if (code == CODE_3INST) return reinterpret_cast<const void*>(&bcjr_codebook_kernel<CODE_3INST>);
+  if (code == CODE_HYB) return reinterpret_cast<const void*>(&bcjr_codebook_kernel<CODE_HYB>);
+  return nullptr;
+}
+
+}  // namespace bcjr

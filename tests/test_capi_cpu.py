@@ -1,0 +1,126 @@
+"""CPU tests of the C ABI library and the host-side logic (no GPU calls).
+
+- libbcjr_hip.so loads and exports every function include/bcjr_hip.h declares;
+- argument validation reports the right status without touching a device;
+- the Python surface keeps the reference's assertion behaviour and layouts.
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "bcjr_hip.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(bcjr_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import bcjr
+    path = bcjr.LIB_PATH
+    if not os.path.exists(path):
+        pytest.fail(f"{path} missing: run __graft_entry__.build()")
+    return bcjr.load_library()
+
+
+def test_header_and_binding_agree():
+    import bcjr._lib as L
+    assert _declared_functions() == sorted(L.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    out = os.popen(f"nm -D --defined-only {lib._name}").read()
+    for name in _declared_functions():
+        assert re.search(rf"\bT {name}\b", out), name
+
+
+def test_strerror_and_version(lib):
+    assert lib.bcjr_version().startswith(b"bcjr_hip")
+    assert lib.bcjr_strerror(0) == b"ok"
+    assert lib.bcjr_strerror(-1) == b"invalid argument"
+    assert lib.bcjr_strerror(-3) == b"workspace too small"
+    assert lib.bcjr_strerror(12345) == b"unknown status"
+
+
+@pytest.mark.parametrize("L,k,V,code,Q,B,N,status,msg", [
+    (16, 3, 1, 0, 9, 4, 256, -2, "k*V=3"),
+    (17, 2, 1, 0, 9, 4, 256, -2, "L=17"),
+    (3, 2, 1, 0, 9, 4, 256, -2, "L=3"),
+    (12, 1, 1, 0, 9, 4, 256, -2, "k*V=1 supports L <= 11"),
+    (16, 2, 3, 0, 9, 4, 256, -1, "V=3"),
+    (16, 2, 1, 0, 9, -1, 256, -1, "B=-1"),
+    (16, 2, 1, 0, 9, 4, 0, -1, "N=0"),
+    (16, 2, 1, 0, 9, 4, 5000, -1, "N=5000"),
+    (16, 2, 2, 1, 9, 4, 128, -1, "1MAD/3INST codes are scalar"),
+    (16, 2, 1, 3, 9, 4, 256, -1, "HYB code is 2-D"),
+    (16, 2, 2, 3, 13, 4, 128, -1, "HYB Q=13"),
+    (16, 2, 1, 7, 9, 4, 256, -1, "unknown code 7"),
+])
+def test_validation_without_device(lib, L, k, V, code, Q, B, N, status, msg):
+    import bcjr._lib as BL
+    p = BL.Problem(L, k, V, B, N, code, Q, 0)
+    n = ctypes.c_size_t(0)
+    rc = lib.bcjr_workspace_bytes(ctypes.byref(p), 0, ctypes.byref(n))
+    assert rc == status
+    assert msg in lib.bcjr_last_error().decode()
+
+
+def test_null_problem(lib):
+    n = ctypes.c_size_t(0)
+    assert lib.bcjr_workspace_bytes(None, 0, ctypes.byref(n)) == -1
+    assert lib.bcjr_forward(None, None, None, None, None, None, None, 0, None) == -1
+
+
+# ------------------------------ host logic --------------------------------
+
+def test_pred_succ_tables_closed_form():
+    from bcjr import build_pred_succ_tables
+    import oracle as O
+    for L, k, V in [(16, 2, 2), (12, 2, 1), (6, 1, 1)]:
+        p, s = build_pred_succ_tables(L, k, V, device="cpu")
+        po, so = O.pred_succ_tables(L, k * V)
+        assert (p.numpy() == po).all() and (s.numpy() == so).all()
+        # every successor of s has s among its predecessors
+        S = 1 << L
+        idx = np.random.default_rng(0).integers(0, S, 64)
+        for st in idx:
+            for nxt in s[st].tolist():
+                assert st in p[nxt].tolist()
+
+
+def test_tile_untile_layout():
+    """(m,n) -> sequences in block order col_block*n_row + row_block, 16x16 row-major
+    (src/qat/ste.py:76-110 numpy form)."""
+    from bcjr.quant import tile_for_viterbi, untile_from_viterbi
+    m, n = 64, 48
+    W = torch.arange(m * n, dtype=torch.float32).reshape(m, n)
+    seqs, info = tile_for_viterbi(W)
+    assert info == (m // 16, n // 16)
+    Wn = W.numpy()
+    for j in range(n // 16):
+        for i in range(m // 16):
+            tile = Wn[i * 16:(i + 1) * 16, j * 16:(j + 1) * 16].reshape(-1)
+            assert (seqs[j * (m // 16) + i].numpy() == tile).all()
+    assert torch.equal(untile_from_viterbi(seqs, info, (m, n)), W)
+
+
+def test_python_surface_asserts_like_reference():
+    from bcjr import bcjr_forward_backward
+    seq = torch.zeros(2, 8, 2)
+    cb = torch.zeros(1 << 6, 2)
+    with pytest.raises(AssertionError):
+        bcjr_forward_backward(torch.zeros(2, 8), cb, 1.0, L=6, k=2, V=2)
+    with pytest.raises(AssertionError):
+        bcjr_forward_backward(seq, torch.zeros(10, 2), 1.0, L=6, k=2, V=2)
+    with pytest.raises(AssertionError):  # CPU tensors: the node runs only on the GPU
+        bcjr_forward_backward(seq, cb, 1.0, L=6, k=2, V=2)

@@ -1,0 +1,209 @@
+"""CPU tests that pin the oracle (oracle/bcjr_oracle.c + oracle/__init__.py).
+
+Each check is independent of the recursion it tests: exhaustive path
+enumeration, finite differences, closed-form limits, the reference's own known
+answers (src/tripwires/test_viterbi.py:17-53, Table-1 bands :77-133, codebook
+bands src/tripwires/test_codes.py:27-98) and golden vectors produced by the
+reference generators (tests/golden/code_vectors.json).
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+from scipy import stats
+
+from conftest import max_rel
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "code_vectors.json")
+
+# (L, kV, V, N, T): tiny trellises brute force can enumerate.
+TINY = [
+    (4, 2, 1, 5, 0.7),
+    (4, 2, 2, 4, 1.3),
+    (6, 2, 1, 5, 0.3),
+    (4, 1, 1, 6, 0.5),
+    (3, 1, 1, 5, 0.2),
+    (8, 4, 2, 3, 1.0),
+    (6, 2, 1, 4, 0.05),
+]
+
+
+@pytest.mark.parametrize("L,KV,V,N,T", TINY)
+def test_forward_matches_brute_force(oracle, L, KV, V, N, T):
+    rng = np.random.default_rng(L * 100 + N)
+    B = 3
+    seq = rng.standard_normal((B, N, V)).astype(np.float32)
+    cb = rng.standard_normal((1 << L, V)).astype(np.float32)
+    soft, logZ = oracle.bcjr_forward(seq, cb, T, L, KV)
+    for b in range(B):
+        bf = oracle.brute_force(seq[b], cb, T, L, KV)
+        assert np.abs(bf["soft"] - soft[b]).max() < 2e-6
+        assert abs(bf["logZ"] - logZ[b]) < 2e-5 * max(1.0, abs(bf["logZ"]))
+
+
+@pytest.mark.parametrize("L,KV,V,N,T", TINY)
+def test_backward_matches_brute_force(oracle, L, KV, V, N, T):
+    rng = np.random.default_rng(7 + L * 100 + N)
+    B = 2
+    seq = rng.standard_normal((B, N, V)).astype(np.float32)
+    cb = rng.standard_normal((1 << L, V)).astype(np.float32)
+    g = rng.standard_normal((B, N, V)).astype(np.float32)
+    gz = rng.standard_normal(B).astype(np.float32)
+    d = oracle.bcjr_backward(seq, cb, T, L, KV, g, gz)
+    for b in range(B):
+        bf = oracle.brute_force(seq[b], cb, T, L, KV, g=g[b], g_logZ=float(gz[b]))
+        assert max_rel(d[b], bf["grad"]) < 1e-6
+
+
+@pytest.mark.parametrize("L,KV,V,N,T", [c for c in TINY if (1 << c[0]) * (1 << c[1]) ** (c[3] - 1) <= 20000][:3])
+def test_brute_force_gradient_is_the_derivative(oracle, L, KV, V, N, T):
+    """The covariance closed form equals central differences of the enumerated loss."""
+    rng = np.random.default_rng(3)
+    seq = rng.standard_normal((N, V))
+    cb = rng.standard_normal((1 << L, V)).astype(np.float32)
+    g = rng.standard_normal((N, V))
+    bf = oracle.brute_force(seq, cb, T, L, KV, g=g, g_logZ=0.7)
+    fd = oracle.finite_difference_grad(seq, cb, T, L, KV, g, 0.7)
+    assert np.abs(fd - bf["grad"]).max() < 1e-6 * max(1.0, np.abs(bf["grad"]).max())
+
+
+@pytest.mark.parametrize("L,KV,V,N,T", [(8, 2, 1, 12, 0.3), (8, 4, 2, 6, 0.8), (10, 2, 1, 16, 0.1)])
+def test_reduced_recursion_matches_reference_gather_form(oracle, L, KV, V, N, T):
+    """C oracle (reduced state) vs the literal gather+logsumexp restatement."""
+    rng = np.random.default_rng(11)
+    seq = rng.standard_normal((2, N, V)).astype(np.float32)
+    cb = rng.standard_normal((1 << L, V)).astype(np.float32)
+    soft, logZ = oracle.bcjr_forward(seq, cb, T, L, KV)
+    s2, z2, P, la, lb = oracle.naive_forward(seq, cb, T, L, KV, return_internals=True)
+    assert np.abs(s2 - soft).max() < 2e-6
+    assert np.abs(z2 - logZ).max() < 2e-5 * np.abs(z2).max()
+    # invariants: marginals sum to 1, LSE(alpha+beta) = logZ at every step
+    assert np.abs(P.sum(-1) - 1.0).max() < 1e-9
+    lse = oracle._lse(la + lb, axis=-1)
+    assert np.abs(lse - z2[:, None]).max() < 1e-9 * np.abs(z2).max()
+
+
+def test_high_temperature_limit(oracle):
+    """T -> inf: P uniform over all states, soft -> mean codeword (forward_backward.py:39-40)."""
+    rng = np.random.default_rng(5)
+    L, KV = 8, 2
+    cb = rng.standard_normal((1 << L, 1)).astype(np.float32)
+    seq = rng.standard_normal((2, 9, 1)).astype(np.float32)
+    soft, _ = oracle.bcjr_forward(seq, cb, 1e7, L, KV)
+    assert np.abs(soft - cb.mean()).max() < 1e-5
+
+
+def test_low_temperature_limit_is_viterbi(oracle):
+    """T -> 0: soft codeword -> Viterbi reconstruction (forward_backward.py:37-38)."""
+    rng = np.random.default_rng(6)
+    L, KV = 8, 2
+    cb = rng.standard_normal((1 << L, 1)).astype(np.float32)
+    seq = rng.standard_normal((3, 20, 1)).astype(np.float32)
+    soft, _ = oracle.bcjr_forward(seq, cb, 1e-4, L, KV)
+    _, _, _, recon, _ = oracle.viterbi(seq, cb, L, KV)
+    assert np.abs(soft - recon).max() < 1e-3
+
+
+def test_gradient_linear_in_upstream(oracle):
+    rng = np.random.default_rng(9)
+    L, KV = 8, 2
+    cb = rng.standard_normal((1 << L, 1)).astype(np.float32)
+    seq = rng.standard_normal((2, 10, 1)).astype(np.float32)
+    g1 = rng.standard_normal(seq.shape).astype(np.float32)
+    g2 = rng.standard_normal(seq.shape).astype(np.float32)
+    d1 = oracle.bcjr_backward(seq, cb, 0.4, L, KV, g1)
+    d2 = oracle.bcjr_backward(seq, cb, 0.4, L, KV, g2)
+    d12 = oracle.bcjr_backward(seq, cb, 0.4, L, KV, g1 + g2)
+    assert max_rel(d1 + d2, d12) < 1e-5
+
+
+# ------------------------------- Viterbi ---------------------------------
+
+def test_viterbi_toy_known_answer(oracle):
+    """src/tripwires/test_viterbi.py:17-53: L=2, k=1 hand-traced walk 00->00->01->11."""
+    cb = np.array([-1.2, -0.3, 0.4, 1.1], np.float32)[:, None]
+    seq = np.array([-1.0, 0.5, 0.8], np.float32)[None, :, None]
+    walk, bits, start, recon, mse = oracle.viterbi(seq, cb, L=2, KV=1)
+    assert np.allclose(recon.ravel(), [-1.2, -0.3, 1.1], atol=1e-6)
+    assert abs(float(((recon - seq) ** 2).sum()) - 0.77) < 1e-4
+    assert walk.tolist() == [[0, 1, 3]] and int(start[0]) == 0 and bits.tolist() == [[0, 1, 1]]
+
+
+def _f32_path_costs(paths, cb, seq1):
+    c = np.zeros(len(paths), np.float32)
+    for t in range(seq1.shape[0]):
+        d = (cb[paths[:, t]] - seq1[t][None]).astype(np.float32)
+        loc = np.zeros(len(paths), np.float32)
+        for v in range(seq1.shape[1]):
+            loc = (loc + (d[:, v] * d[:, v]).astype(np.float32)).astype(np.float32)
+        c = (c + loc).astype(np.float32)
+    return c
+
+
+@pytest.mark.parametrize("L,KV,V,N", [(4, 2, 1, 5), (4, 2, 2, 4), (5, 1, 1, 6), (6, 2, 1, 4), (8, 4, 2, 3)])
+def test_viterbi_is_min_cost_path(oracle, L, KV, V, N):
+    rng = np.random.default_rng(L + N)
+    paths = oracle.enumerate_paths(L, KV, N)
+    for _ in range(20):
+        cb = rng.standard_normal((1 << L, V)).astype(np.float32)
+        seq = rng.standard_normal((1, N, V)).astype(np.float32)
+        walk, bits, start, recon, mse = oracle.viterbi(seq, cb, L, KV)
+        c = _f32_path_costs(paths, cb, seq[0])
+        idx = np.where((paths == walk[0][None]).all(1))[0]
+        assert len(idx) == 1 and c[idx[0]] == c.min()
+        w2, r2 = oracle.decode(bits, start, cb, L, KV)
+        assert (w2 == walk).all() and (r2 == recon).all()
+
+
+def test_viterbi_tie_rules(oracle):
+    """All-equal codewords: every path ties.  Lowest p at every step and lowest
+    final state give the all-zero walk (encode.py:283-296)."""
+    L, KV, N = 4, 2, 5
+    cb = np.zeros((1 << L, 1), np.float32)
+    seq = np.ones((1, N, 1), np.float32)
+    walk, bits, start, _, _ = oracle.viterbi(seq, cb, L, KV)
+    assert walk.tolist() == [[0] * N] and int(start[0]) == 0
+    # Two tied minima at the last step: the lower state index wins.
+    cb = np.full((1 << L, 1), 5.0, np.float32)
+    cb[3] = cb[9] = 1.0
+    seq = np.ones((1, 1, 1), np.float32)
+    walk, _, start, _, _ = oracle.viterbi(seq, cb, L, KV)
+    assert int(walk[0, 0]) == 3 and int(start[0]) == 0
+
+
+def test_viterbi_table1_band_1mad(oracle):
+    """Table-1 MSE band for 1MAD at L=16, k=2 (src/tripwires/test_viterbi.py:77-133)."""
+    rng = np.random.default_rng(42)
+    cb = oracle.codebook(oracle.CODE_1MAD, 16)
+    seq = rng.standard_normal((16, 256, 1)).astype(np.float32)
+    _, _, _, _, mse = oracle.viterbi(seq, cb, 16, 2)
+    assert 0.062 <= float(mse.mean()) <= 0.075
+
+
+# ------------------------------- codebooks -------------------------------
+
+@pytest.mark.parametrize("name,code", [("1mad", 1), ("3inst", 2), ("hyb", 3)])
+def test_codebook_golden(oracle, name, code):
+    g = json.load(open(GOLDEN))
+    lut = np.random.default_rng(g["hyb_lut_seed"]).standard_normal((512, 2)).astype(np.float32)
+    cb = oracle.codebook(code, g["L"], lut=lut if code == 3 else None)
+    ref = g["codes"][name]
+    assert hashlib.sha256(cb.tobytes()).hexdigest() == ref["sha256_f32"]
+    assert cb[np.asarray(g["sample_states"])].view(np.uint32).tolist() == ref["sample_bits"]
+
+
+@pytest.mark.parametrize("code", [1, 2])
+def test_codebook_marginals(oracle, code):
+    """src/tripwires/test_codes.py:27-40 bands."""
+    cb = oracle.codebook(code, 16)[:, 0]
+    assert abs(cb.mean()) < 0.05 and 0.85 < cb.var() < 1.15
+    assert 2.6 < stats.kurtosis(cb, fisher=False) < 3.4
+
+
+def test_pack_roundtrip(oracle):
+    rng = np.random.default_rng(0)
+    for KV in (1, 2, 4):
+        bits = rng.integers(0, 1 << KV, size=(5, 37)).astype(np.int32)
+        assert (oracle.unpack_bits(oracle.pack_bits(bits, KV), 37, KV) == bits).all()
