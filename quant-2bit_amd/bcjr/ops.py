@@ -47,12 +47,28 @@ def _workspace(prob: _lib.Problem, op: int, device: torch.device) -> torch.Tenso
     return torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=device)
 
 
+_T_CACHE: dict = {}
+
+
+def _scalar_T(value: float, device: torch.device) -> torch.Tensor:
+    """Device copy of a python-float temperature, made once per (device, value), so
+    steady-state calls (and calls under graph capture) do no host-to-device copy."""
+    key = (str(device), float(value))
+    t = _T_CACHE.get(key)
+    if t is None:
+        if len(_T_CACHE) > 256:
+            _T_CACHE.clear()
+        t = torch.tensor([float(value)], dtype=torch.float32, device=device)
+        _T_CACHE[key] = t
+    return t
+
+
 def _temperature(T, B: int, device: torch.device):
     """float32 device tensor holding one T, or B of them; returns (tensor, per_seq)."""
     if torch.is_tensor(T):
         Tt = T.detach().to(device=device, dtype=torch.float32).reshape(-1).contiguous()
     else:
-        Tt = torch.tensor([float(T)], dtype=torch.float32, device=device)
+        Tt = _scalar_T(T, device)
     if Tt.numel() == 1:
         return Tt, False
     if Tt.numel() != B:

@@ -7,7 +7,7 @@
 //   cum_0 = 0;  cum_t(s) = fl( min_p cum_{t-1}(p*NT + (s >> kV)) + E_t(s) ),
 //   E_t(s)  = fl( sum_v fl( fl(c_v(s) - w_t[v])^2 ) )     (no FMA contraction),
 //   the lowest p wins a tie, the lowest final state wins a tie,
-//   walk_{t-1} = bp_t(walk_t >> kV) * NT + (walk_t >> kV),
+//   walk_{t-1} = argmin_p cum_{t-1}(p*NT + (walk_t >> kV)) * NT + (walk_t >> kV),
 //   start = bp_0(walk_0 >> kV) * NT + (walk_0 >> kV) = walk_0 >> kV,
 //   bitstream_t = walk_t & (2^kV - 1), recon_t = c(walk_t).
 // Min-sum has no transcendentals; the butterfly layout and the per-step LDS
@@ -190,12 +190,15 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
     }
     __syncthreads();
 
-    // Traceback: stage up to 8 backpointer rows in LDS, walk them on one thread.
+    // Traceback.  Row t of bp holds argmin_p cum_t(p*NT + j), i.e. the best
+    // predecessor of the states of step t+1, so walk_{t} = bp_t(walk_{t+1} >> kV)
+    // * NT + (walk_{t+1} >> kV).  Rows are staged in LDS, up to 8 at a time, and
+    // walked on one thread.
     const int cap = (int)((2 * (size_t)NT * sizeof(float)) / (size_t)NT);
     uint8_t* stage = reinterpret_cast<uint8_t*>(rbuf);
     int s = walkbuf[N - 1];
-    for (int hi = N - 1; hi >= 1; hi -= cap) {
-      const int lo = max(1, hi - cap + 1);
+    for (int hi = N - 2; hi >= 0; hi -= cap) {
+      const int lo = max(0, hi - cap + 1);
       const int nbytes_rows = (hi - lo + 1) * NT;
       if ((NT & 3) == 0) {
         const uint32_t* srcw = reinterpret_cast<const uint32_t*>(bp + (size_t)lo * NT);
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
         for (int t = hi; t >= lo; --t) {
           const int j = s >> KV;
           s = (int)stage[(size_t)(t - lo) * NT + j] * NT + j;
-          walkbuf[t - 1] = s;
+          walkbuf[t] = s;
         }
       }
       __syncthreads();

@@ -81,7 +81,7 @@ def test_forward_backward_tiny_vs_brute_force(bcjr_mod, oracle, L, k, V, N, T):
     for b in range(seq.shape[0]):
         bf = oracle.brute_force(seq[b], cb, T, L, k * V, g=g[b])
         assert max_rel(soft[b].detach().cpu().numpy(), bf["soft"]) < SOFT_TOL
-        assert abs(float(logZ[b]) - bf["logZ"]) <= LOGZ_TOL * max(1.0, abs(bf["logZ"]))
+        assert abs(float(logZ[b].detach()) - bf["logZ"]) <= LOGZ_TOL * max(1.0, abs(bf["logZ"]))
         assert max_rel(x.grad[b].cpu().numpy(), bf["grad"]) < GRAD_TOL
 
 
@@ -100,6 +100,7 @@ CASES = [
     (10, 1, 2, 64, 4, "hyb", 0.4),       # k = 1, V = 2 (kV = 2, 2-D)
     (16, 2, 1, 256, 2, "3inst", 0.1),    # single-tile config: L=16, 8 butterflies per thread
     (16, 2, 1, 96, 2, "1mad", 0.05),
+    (16, 2, 1, 128, 2, "3inst", 0.01),   # the float32 floor the reference states (T >= 1e-2)
     (16, 2, 2, 64, 2, "hyb", 0.1),       # reference QAT trellis (L=16, kV=4)
 ]
 
@@ -312,10 +313,28 @@ def test_full_size_properties(bcjr_mod):
         (s * g).sum().backward()
         grads.append(xs.grad.clone())
     assert max_rel((grads[0] + grads[1]).cpu().numpy(), grads[2].cpu().numpy()) < 1e-4
-    # low T approaches the Viterbi reconstruction
-    s_lo, _ = bcjr_forward_backward(x[:32], cb, 1e-3, L=16, k=2, V=1)
-    _, _, recon, _ = viterbi_encode_v_batched_hip(x[:32, :, 0].contiguous(), cb, L=16, k=2, V=1)
-    assert (s_lo[:, :, 0] - recon).abs().max() < 2e-2
+    # T -> 0 approaches the Viterbi reconstruction wherever the best path is not
+    # tied to within ~T (at T=1e-3 about 0.3-1.2% of positions still mix, in the
+    # float64 oracle too)
+    s_lo, _ = bcjr_forward_backward(x[:64], cb, 1e-3, L=16, k=2, V=1)
+    _, _, recon, _ = viterbi_encode_v_batched_hip(x[:64, :, 0].contiguous(), cb, L=16, k=2, V=1)
+    diff = (s_lo[:, :, 0] - recon).abs()
+    assert float((diff > 1e-2).float().mean()) < 0.05
+    assert float(diff.median()) < 1e-4
+
+
+def test_low_temperature_precision_bound(bcjr_mod, oracle):
+    """Below T = 1e-2 float32 log-domain recursions lose precision as 1/T (the
+    alpha/beta of a state on the final best path can lie ~1e4/T log2-units below
+    the per-step maximum).  Record the bound: 2e-3 at T = 1e-3 (1e-4 holds for
+    T >= 1e-2, see the parity cases)."""
+    _say("low-T precision bound")
+    from bcjr import bcjr_forward_backward, make_3inst_codebook
+    cb = make_3inst_codebook(16, "cuda")
+    x = np.random.default_rng(0).standard_normal((4, 256, 1)).astype(np.float32)
+    soft, _ = bcjr_forward_backward(torch.tensor(x, device="cuda"), cb, 1e-3, L=16, k=2, V=1)
+    s_ref, _ = oracle.bcjr_forward(x, cb.cpu().numpy(), 1e-3, 16, 2)
+    assert max_rel(soft.cpu().numpy(), s_ref) < 2e-3
 
 
 def test_graph_capture_replays(bcjr_mod):
@@ -324,27 +343,29 @@ def test_graph_capture_replays(bcjr_mod):
     from bcjr import bcjr_forward_backward, make_1mad_codebook
     L, B, N = 12, 16, 256
     cb = make_1mad_codebook(L, "cuda")
+    T = torch.tensor(0.1, device="cuda")  # a 0-d device buffer, as QuantizedLinear.T_temp
     x = torch.randn(B, N, 1, device="cuda", requires_grad=True)
     g = torch.randn(B, N, 1, device="cuda")
-    soft, _ = bcjr_forward_backward(x, cb, 0.1, L=L, k=2, V=1)
-    (soft * g).sum().backward()
+    soft, _ = bcjr_forward_backward(x, cb, T, L=L, k=2, V=1)
+    soft.backward(g)
     ref_soft, ref_grad = soft.detach().clone(), x.grad.clone()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        for _ in range(2):  # warm the allocator outside the capture
-            x.grad = None
-            out, _ = bcjr_forward_backward(x, cb, 0.1, L=L, k=2, V=1)
-            (out * g).sum().backward()
+        xg = x.detach().clone().requires_grad_(True)  # fresh leaf: its grad node lives on s
+        for _ in range(2):  # warm the allocator and the launch-plan cache outside the capture
+            xg.grad = None
+            out, _ = bcjr_forward_backward(xg, cb, T, L=L, k=2, V=1)
+            out.backward(g)
     torch.cuda.current_stream().wait_stream(s)
     graph = torch.cuda.CUDAGraph()
-    x.grad = None
+    xg.grad = None
     with torch.cuda.graph(graph):
-        out, _ = bcjr_forward_backward(x, cb, 0.1, L=L, k=2, V=1)
-        (out * g).sum().backward()
+        out, _ = bcjr_forward_backward(xg, cb, T, L=L, k=2, V=1)
+        out.backward(g)
     for _ in range(3):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.detach(), ref_soft)
-        assert max_rel(x.grad.cpu().numpy(), ref_grad.cpu().numpy()) < 1e-5
+        assert torch.equal(xg.grad, ref_grad)
         _ = torch.randn(1024, device="cuda").sum().item()  # eager work between replays
