@@ -15,39 +15,59 @@
 // Then d seq_t[v] = (2/T) (sum_s dll_t(s) c_v(s) - w_t[v] sum_s dll_t(s)), the
 // chain rule through ll = -||c - w||^2 / T used in bcjr_monolithic.py:228-239.
 //
+// Log-sum-exps use the butterfly-normalised group sums of the forward kernel;
+// codewords are formed per state from the hash (c = kSigma * h),
+// so f_t(s) = (kSigma g_t) . h(s) and the sums over h are scaled once at the end.
+//
 // Two vectors (m~, mu) or (n~, nu) of NT floats move through LDS each step, which
-// at L = 16 fills 128 KiB; they are single-buffered, so each step reads all of a
-// thread's inputs, synchronises, then computes and writes.  The alpha sweep writes
-// each butterfly's normalised inputs (m~ and mu, 2R floats) to the scratch slot;
-// the beta sweep reads them back to form P and phi.
+// at L = 16 fills 128 KiB, so they are single-buffered, interleaved as 8-byte
+// pairs, in the in-place rotated layout of Swizzle: a thread reads its
+// butterfly's R pairs, computes, and writes its R outputs to the same pairs, with
+// one barrier per step and the next butterfly's pairs read ahead of the current
+// one's arithmetic.  The alpha sweep writes each butterfly's raw inputs (m~ and
+// mu, 2R floats) to the scratch slot; the beta sweep reads them back two
+// butterflies ahead to form P and phi.
+//
+// Group sums take the zero-shift form; a butterfly with any
+// underflowed group (sum < kUnderflow) is recomputed against the group maxima
+// (rare at T >= kExactBelowT; below it every group uses the maxima).
 #include "bcjr_device.h"
 #include "bcjr_kernels.h"
 
 namespace bcjr {
 
+// Unroll of the loop over a butterfly's outputs: full for 2 or 4 states.
+template <int R>
+constexpr int kOuterUnroll = R <= 4 ? R : 1;
+
 template <int KV, int V, int CODE, int UPT>
 __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
   constexpr int R = 1 << KV;
-  constexpr int RO = R < 4 ? R : 4;
-  constexpr int NSUB = R / RO;
+  using CT = CodeTraits<CODE>;
+  // Butterflies of 2 or 4 states run fully unrolled with their slot-side
+  // inputs prefetched in registers; 16-state butterflies loop over outputs and
+  // read those inputs from the slot as they go.
+  constexpr bool kPair = R <= 4;
 
   extern __shared__ __align__(16) unsigned char smem[];
   const int L = P.L, N = P.N;
-  const int NT = 1 << (L - KV);
+  const int nb = L - KV;  // reduced-state bits
+  const int NT = 1 << nb;
   const int NB = NT >> KV;
-  const int NU = NB * NSUB;
-  const int lgNB = L - 2 * KV;
+  const uint32_t ANT = opaque_uniform(CT::A * (uint32_t)NT);  // hash offset of p * NT
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
+  const Swizzle swz = P.swz;
 
-  double* cvec = reinterpret_cast<double*>(smem);  // N
-  float* mbuf = reinterpret_cast<float*>(cvec + N);  // NT (m~, then n~)
-  float* mubuf = mbuf + NT;                          // NT (mu, then nu)
-  float* wmax = mubuf + NT;                          // 2*kMaxWaves
-  float* wsum = wmax + 2 * kMaxWaves;                // 2*kMaxWaves
-  float* wbuf = wsum + 2 * kMaxWaves;                // N*V
-  float* gbuf = wbuf + N * V;                        // N*V
-  float* apart = gbuf + N * V;                       // N*nwaves*(V+1)
+  // LDS: the (m~, mu) pairs sit at byte 0, so a pair's byte address is 8 times
+  // its element index.
+  float2* mm = reinterpret_cast<float2*>(smem);                    // NT (m~, mu) then (n~, nu)
+  double* cvec = reinterpret_cast<double*>(smem + (size_t)8 * NT);  // N  C_{t-1}
+  float* wmax = reinterpret_cast<float*>(cvec + ((N + 1) & ~1));    // 2*kMaxWaves
+  float* wsum = wmax + 2 * kMaxWaves;                               // 2*kMaxWaves
+  float* wbuf = wsum + 2 * kMaxWaves;                               // N*V
+  float* gbuf = wbuf + N * V;                                       // N*V
+  float* apart = gbuf + N * V;                                      // N*nwaves*(V+1)
   float* lut = apart + N * nwaves * (V + 1);
 
   if constexpr (CODE == CODE_HYB) {
@@ -56,10 +76,26 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
     __syncthreads();
   }
 
+  // Byte address of slot k of butterfly tid + i*nthr at rotation rho:
+  // 8 S(rotr(tid + i*nthr + k*NB)) = yb ^ unit_off(i) ^ slot_off(k), the last
+  // two uniform (tid, i*nthr and k*NB occupy disjoint bits; S and rotr are
+  // linear).
+  auto base_off = [&](int rho) -> uint32_t {
+    return swizzle(rotr_bits((uint32_t)min(tid, NB - 1), rho, nb), swz) << 3;
+  };
+  auto unit_off = [&](int i, int rho) -> uint32_t {
+    return swizzle(rotr_bits((uint32_t)(i * nthr), rho, nb), swz) << 3;
+  };
+  auto slot_off = [&](int k, int rho) -> uint32_t {
+    return swizzle(rotr_bits((uint32_t)(k * NB), rho, nb), swz) << 3;
+  };
+  auto lds_pair = [&](uint32_t off) -> float2& { return *reinterpret_cast<float2*>(smem + off); };
+
   for (long long b = blockIdx.x; b < P.B; b += gridDim.x) {
     float* slot = P.ws + (size_t)blockIdx.x * (size_t)N * 2 * (size_t)NT;
     const float Tb = P.T[P.t_per_seq ? b : 0];
     const float sk = sqrtf(kLog2e / Tb);
+    const float ssk = CT::kSigma * sk;
     const float gZ = P.g_logZ ? P.g_logZ[b] : 0.0f;
     const float* seqb = P.seq + (size_t)b * N * V;
     const float* gb = P.g_soft + (size_t)b * N * V;
@@ -69,221 +105,429 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
     }
     __syncthreads();
 
-    // --------------------------- alpha + mu sweep ----------------------------
-    double C = 0.0;
-    int k = 0;
-    for (int t = 0; t < N; ++t, ++k) {
-      float O = (float)KV;
-      if (t > 0) {
-        O = -INFINITY;
-        for (int w = 0; w < nwaves; ++w) O = fmaxf(O, wmax[((k + 1) & 1) * kMaxWaves + w]);
-      }
-      C += (double)O;
-      if (tid == 0) cvec[t] = C;
-      float nw[V], gt[V];
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        nw[v] = -wbuf[t * V + v] * sk;
-        gt[v] = gbuf[t * V + v];
-      }
-      float mi[UPT][R], mui[UPT][R];
-#pragma unroll
-      for (int i = 0; i < UPT; ++i) {
-        const int u = opaque(tid + i * nthr) & (NB - 1);
-#pragma unroll
-        for (int p = 0; p < R; ++p) {
-          mi[i][p] = t ? mbuf[p * NB + u] - O : 0.0f;
-          mui[i][p] = t ? mubuf[p * NB + u] : 0.0f;
+    // Below kExactBelowT most groups would underflow the zero-shift sums, so
+    // the whole sequence uses the group maxima.  The choice is a uniform branch
+    // around both sweeps: each variant gets its own register allocation.
+    auto sweeps = [&](auto exact_tag) {
+      constexpr bool EXACT = decltype(exact_tag)::value;
+      using Fast = std::integral_constant<bool, EXACT>;
+
+      // --------------------------- alpha + mu sweep ----------------------------
+      double C = 0.0;  // C_{t-1}
+      int k = 0;
+      int rho = nb - KV;  // kV * (t - 1) mod nb at t = 0
+      for (int t = 0; t < N; ++t, ++k) {
+        float O = (float)KV;
+        if (t > 0) {
+          O = -INFINITY;
+          for (int w = 0; w < nwaves; ++w) O = fmaxf(O, wmax[((k + 1) & 1) * kMaxWaves + w]);
         }
-      }
-      __syncthreads();
-      float tmax = -INFINITY;
+        if (tid == 0) cvec[t] = C;
+        C += (double)O;
+        float nw[V], sg[V];
 #pragma unroll
-      for (int i = 0; i < UPT; ++i) {
-        const int q = tid + i * nthr;
-        __builtin_amdgcn_sched_barrier(0);
-        if (q < NU) {
-          const int u = opaque(q) & (NB - 1);
-          const int sub = q >> lgNB;
-          if (sub == 0) {
-            float* dst = slot + ((size_t)t * NB + u) * 2 * R;
+        for (int v = 0; v < V; ++v) {
+          nw[v] = -wbuf[t * V + v] * sk;
+          sg[v] = CT::kSigma * gbuf[t * V + v];  // f = g . c = sg . h
+        }
+        const uint32_t yb = base_off(rho);
+        uint32_t Ku[UPT], Kk[R];  // uniform per step
 #pragma unroll
-            for (int p = 0; p < R; ++p) {
-              dst[p] = mi[i][p];
-              dst[R + p] = mui[i][p];
-            }
+        for (int i = 0; i < UPT; ++i) Ku[i] = unit_off(i, rho);
+        if constexpr (kPair) {
+#pragma unroll
+          for (int c = 0; c < R; ++c) Kk[c] = slot_off(c, rho);
+        }
+        auto koff = [&](int c) -> uint32_t {
+          if constexpr (kPair) {
+            return Kk[c];
+          } else {
+            return slot_off(c, rho);
           }
-          float mo[RO], muo[RO];
+        };
+
+        // Output r of butterfly u: m~ and mu of state R*u + r from the shifted
+        // inputs m[p] (maximum 0) and the raw mu inputs; returns the group sum.
+        auto alpha_out = [&](auto shift_tag, int r, uint32_t xu, int u, const float (&m)[R],
+                             const float (&mui)[R], float oout, float& mo, float& muo) -> float {
+          constexpr bool SHIFT = decltype(shift_tag)::value;
+          float a[R], phi[R];
 #pragma unroll
-          for (int r = 0; r < RO; ++r) {
-            const int rr = sub * RO + r;
-            float a[R], phi[R];
+          for (int p = 0; p < R; ++p) {
+            float h[V];
+            raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)r, (uint32_t)(p * NT + R * u + r), P.table,
+                                  lut, P.Q, h);
+            float acc = m[p];
+            float ph = mui[p];
 #pragma unroll
-            for (int p = 0; p < R; ++p) {
-              float c[V];
-              codeword<CODE, V, false>((uint32_t)(p * NT + R * u + rr), P.table, lut, P.Q, c);
-              float acc = mi[i][p];
-              float ph = mui[i][p];
-#pragma unroll
-              for (int v = 0; v < V; ++v) {
-                const float d = fmaf(c[v], sk, nw[v]);
-                acc = fmaf(-d, d, acc);
-                ph = fmaf(gt[v], c[v], ph);
-              }
-              a[p] = acc;
-              phi[p] = ph;
+            for (int v = 0; v < V; ++v) {
+              const float d = fmaf(h[v], ssk, nw[v]);
+              acc = fmaf(-d, d, acc);
+              ph = fmaf(sg[v], h[v], ph);
             }
-            float M = a[0];
+            a[p] = acc;
+            phi[p] = ph;
+          }
+          float M = 0.0f;
+          if constexpr (SHIFT) {
+            M = a[0];
 #pragma unroll
             for (int p = 1; p < R; ++p) M = fmaxf(M, a[p]);
-            float ssum = 0.0f, ephi = 0.0f;
+          }
+          float e = fexp2(a[0] - M);
+          float s = e, ephi = e * phi[0];
 #pragma unroll
-            for (int p = 0; p < R; ++p) {
-              const float e = fexp2(a[p] - M);
-              ssum += e;
-              ephi = fmaf(e, phi[p], ephi);
+          for (int p = 1; p < R; ++p) {
+            e = fexp2(a[p] - M);
+            s += e;
+            ephi = fmaf(e, phi[p], ephi);
+          }
+          mo = flog2(s) + (M - oout);
+          muo = ephi * frcp(s);
+          return s;
+        };
+
+        auto read_in = [&](int i, float (&m)[R], float (&mu)[R]) {
+          const uint32_t yi = yb ^ Ku[i];
+#pragma unroll
+          for (int p = 0; p < R; ++p) {
+            if (t) {
+              const float2 v2 = lds_pair(yi ^ koff(p));
+              m[p] = v2.x;
+              mu[p] = v2.y;
+            } else {
+              m[p] = (float)KV;
+              mu[p] = 0.0f;
             }
-            mo[r] = M + flog2(ssum);
-            muo[r] = ephi * frcp(ssum);
-            tmax = fmaxf(tmax, mo[r]);
           }
+        };
+        // Inputs of the next butterfly are read before the current one's
+        // arithmetic: its pairs are disjoint from every pair written here.
+        float nx[R], nxu[R];
+        read_in(0, nx, nxu);
+        float tmax = -INFINITY;
 #pragma unroll
-          for (int r = 0; r < RO; ++r) {
-            mbuf[R * u + sub * RO + r] = mo[r];
-            mubuf[R * u + sub * RO + r] = muo[r];
+        for (int i = 0; i < UPT; ++i) {
+          const int q = tid + i * nthr;
+          float mi[R], mui[R];
+#pragma unroll
+          for (int p = 0; p < R; ++p) {
+            mi[p] = nx[p];
+            mui[p] = nxu[p];
           }
-        }
-      }
-      tmax = wave_max(tmax);
-      if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
-      __syncthreads();
-    }
-
-    // log2 Z and E[F] = sum_j 2^(m_{N-1}(j) - log2 Z) mu_{N-1}(j).
-    float Mz = -INFINITY;
-    for (int w = 0; w < nwaves; ++w) Mz = fmaxf(Mz, wmax[((k + 1) & 1) * kMaxWaves + w]);
-    float ps = 0.0f, pe = 0.0f;
-    for (int j = tid; j < NT; j += nthr) {
-      const float e = fexp2(mbuf[j] - Mz);
-      ps += e;
-      pe = fmaf(e, mubuf[j], pe);
-    }
-    ps = wave_sum(ps);
-    pe = wave_sum(pe);
-    if (lane == 0) {
-      wsum[wave] = ps;
-      wsum[kMaxWaves + wave] = pe;
-    }
-    __syncthreads();
-    float Ssum = 0.0f, Esum = 0.0f;
-    for (int w = 0; w < nwaves; ++w) {
-      Ssum += wsum[w];
-      Esum += wsum[kMaxWaves + w];
-    }
-    const double logZ2 = C + (double)Mz + (double)flog2(Ssum);
-    const float EF = Esum / Ssum;
-
-    // -------------------------- beta + nu + grad sweep -----------------------
-    double D = 0.0;
-    for (int t = N - 1; t >= 0; --t, ++k) {
-      float Qv = 0.0f;
-      if (t != N - 1) {
-        Qv = -INFINITY;
-        for (int w = 0; w < nwaves; ++w) Qv = fmaxf(Qv, wmax[((k + 1) & 1) * kMaxWaves + w]);
-      }
-      const float Kt = (float)(cvec[t] + (double)Qv + D - logZ2);
-      float nw[V], gt[V];
+          if (i + 1 < UPT) read_in(i + 1, nx, nxu);
+          __builtin_amdgcn_sched_barrier(0);
+          if (q < NB) {
+            const int u = opaque(q);
+            {
+              float* dst = slot + ((size_t)t * NB + u) * 2 * R;
+              store_vec<R>(dst, mi);
+              store_vec<R>(dst + R, mui);
+            }
+            float Mu = mi[0];
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        nw[v] = -wbuf[t * V + v] * sk;
-        gt[v] = gbuf[t * V + v];
-      }
-      float ni[UPT][R], nui[UPT][R];
+            for (int p = 1; p < R; ++p) Mu = fmaxf(Mu, mi[p]);
+            const float sh = -Mu;
+            float m[R];
 #pragma unroll
-      for (int i = 0; i < UPT; ++i) {
-        const int u = opaque(tid + i * nthr) & (NB - 1);
+            for (int p = 0; p < R; ++p) m[p] = mi[p] + sh;
+            const uint32_t xu = CT::A * (uint32_t)(R * u) + CT::B;
+            const float oout = sh + O;
+            const uint32_t yi = yb ^ Ku[i];
+            if constexpr (kPair) {
+              float mo[R], muo[R], smin = 0.0f;
 #pragma unroll
-        for (int c = 0; c < R; ++c) {
-          ni[i][c] = (t != N - 1) ? mbuf[R * u + c] - Qv : 0.0f;
-          nui[i][c] = (t != N - 1) ? mubuf[R * u + c] : 0.0f;
-        }
-      }
-      __syncthreads();
-      float A0 = 0.0f, A1[V];
-#pragma unroll
-      for (int v = 0; v < V; ++v) A1[v] = 0.0f;
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < UPT; ++i) {
-        const int q = tid + i * nthr;
-        __builtin_amdgcn_sched_barrier(0);
-        if (q < NU) {
-          const int u = opaque(q) & (NB - 1);
-          const int sub = q >> lgNB;
-          const float* src = slot + ((size_t)t * NB + u) * 2 * R + sub * RO;
-          float m4[RO], mu4[RO];
-#pragma unroll
-          for (int pp = 0; pp < RO; ++pp) {
-            m4[pp] = src[pp];
-            mu4[pp] = src[R + pp];
-          }
-#pragma unroll
-          for (int pp = 0; pp < RO; ++pp) {
-            const int p = sub * RO + pp;
-            float y[R], z[R], cc[R][V];
-#pragma unroll
-            for (int c = 0; c < R; ++c) {
-              codeword<CODE, V, false>((uint32_t)(p * NT + R * u + c), P.table, lut, P.Q, cc[c]);
-              float yy = ni[i][c];
-              float zz = nui[i][c];
-#pragma unroll
-              for (int v = 0; v < V; ++v) {
-                const float d = fmaf(cc[c][v], sk, nw[v]);
-                yy = fmaf(-d, d, yy);
-                zz = fmaf(gt[v], cc[c][v], zz);
+              for (int r = 0; r < R; ++r) {
+                const float s = alpha_out(Fast{}, r, xu, u, m, mui, oout, mo[r], muo[r]);
+                smin = r ? fminf(smin, s) : s;
               }
-              y[c] = yy;
-              z[c] = zz;
+              if constexpr (!EXACT) {
+                if (smin < kUnderflow) {
+#pragma unroll
+                  for (int r = 0; r < R; ++r) alpha_out(std::true_type{}, r, xu, u, m, mui, oout, mo[r], muo[r]);
+                }
+              }
+#pragma unroll
+              for (int r = 0; r < R; ++r) {
+                lds_pair(yi ^ koff(r)) = make_float2(mo[r], muo[r]);
+                tmax = fmaxf(tmax, mo[r]);
+              }
+            } else {
+#pragma unroll kOuterUnroll<R>
+              for (int r = 0; r < R; ++r) {
+                float mo, muo;
+                const float s = alpha_out(Fast{}, r, xu, u, m, mui, oout, mo, muo);
+                if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, r, xu, u, m, mui, oout, mo, muo);
+                lds_pair(yi ^ koff(r)) = make_float2(mo, muo);
+                tmax = fmaxf(tmax, mo);
+              }
             }
-            float M = y[0];
+          }
+        }
+        tmax = wave_max(tmax);
+        if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
+        rho = rho + KV >= nb ? rho + KV - nb : rho + KV;
+        __syncthreads();
+      }
+
+      // log2 Z and E[F] = sum_j 2^(m_{N-1}(j) - log2 Z) mu_{N-1}(j); m~ and mu of a
+      // state share a pair, so the sums run over pairs.
+      float Mz = -INFINITY;
+      for (int w = 0; w < nwaves; ++w) Mz = fmaxf(Mz, wmax[((k + 1) & 1) * kMaxWaves + w]);
+      float ps = 0.0f, pe = 0.0f;
+      for (int j = tid; j < NT; j += nthr) {
+        const float2 v2 = mm[j];
+        const float e = fexp2(v2.x - Mz);
+        ps += e;
+        pe = fmaf(e, v2.y, pe);
+      }
+      ps = wave_sum(ps);
+      pe = wave_sum(pe);
+      if (lane == 0) {
+        wsum[wave] = ps;
+        wsum[kMaxWaves + wave] = pe;
+      }
+      __syncthreads();
+      float Ssum = 0.0f, Esum = 0.0f;
+      for (int w = 0; w < nwaves; ++w) {
+        Ssum += wsum[w];
+        Esum += wsum[kMaxWaves + w];
+      }
+      const double logZ2 = C + (double)Mz + (double)flog2(Ssum);
+      const float EFg = Esum / Ssum - gZ;  // E[F] - g_Z
+
+      // -------------------------- beta + nu + grad sweep -----------------------
+      // Raw alpha-side inputs (m~, mu) of step t come back from HBM two
+      // butterflies ahead of their use, across step boundaries.
+      auto slot_src = [&](int t, int i) {
+        const int q = min(tid + i * nthr, NB - 1);
+        return slot + ((size_t)t * NB + q) * 2 * R;
+      };
+      float pa[R], pua[R], pb[R], pub[R];  // the next two butterflies in consumption order
+      if (kPair) {
+        load_vec<R>(slot_src(N - 1, 0), pa);
+        load_vec<R>(slot_src(N - 1, 0) + R, pua);
+      }
+      if (kPair && (UPT > 1 || N > 1)) {
+        const float* src = UPT > 1 ? slot_src(N - 1, 1) : slot_src(N - 2, 0);
+        load_vec<R>(src, pb);
+        load_vec<R>(src + R, pub);
+      }
+      double D = 0.0;  // D_t
+      // rho_t = kV * (t - 1) mod nb at t = N - 1
+      rho = (int)(((long long)KV * (N - 2) % nb + nb) % nb);
+      for (int t = N - 1; t >= 0; --t, ++k) {
+        float Qv = 0.0f;
+        if (t != N - 1) {
+          Qv = -INFINITY;
+          for (int w = 0; w < nwaves; ++w) Qv = fmaxf(Qv, wmax[((k + 1) & 1) * kMaxWaves + w]);
+        }
+        const float Kt = (float)(cvec[t] + D - logZ2);
+        float nw[V], sg[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          nw[v] = -wbuf[t * V + v] * sk;
+          sg[v] = CT::kSigma * gbuf[t * V + v];
+        }
+        const uint32_t yb = base_off(rho);
+        uint32_t Ku[UPT], Kk[R];  // uniform per step
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) Ku[i] = unit_off(i, rho);
+        if constexpr (kPair) {
+#pragma unroll
+          for (int c = 0; c < R; ++c) Kk[c] = slot_off(c, rho);
+        }
+        auto koff = [&](int c) -> uint32_t {
+          if constexpr (kPair) {
+            return Kk[c];
+          } else {
+            return slot_off(c, rho);
+          }
+        };
+
+        // Output p of butterfly u: n~ and nu of state p*NB + u from the shifted
+        // inputs nr[c] (maximum 0) and raw nu inputs, and the butterfly's
+        // contribution to the gradient sums (a0 for sum dll, a1 for sum dll h).
+        // pms = raw m~_{t-1}(p*NB + u) + Kt - sh.  Returns the group sum.
+        auto beta_out = [&](auto shift_tag, int p, uint32_t xu, int u, const float (&nr)[R],
+                            const float (&nui)[R], float pms, float pmu, float oout, float& no, float& nuo,
+                            float& a0, float (&a1)[V]) -> float {
+          constexpr bool SHIFT = decltype(shift_tag)::value;
+          float y[R], z[R], hh[R][V];
+#pragma unroll
+          for (int c = 0; c < R; ++c) {
+            raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)c, (uint32_t)(p * NT + R * u + c), P.table,
+                                  lut, P.Q, hh[c]);
+            float yy = nr[c];
+            float zz = nui[c];
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              const float d = fmaf(hh[c][v], ssk, nw[v]);
+              yy = fmaf(-d, d, yy);
+              zz = fmaf(sg[v], hh[c][v], zz);
+            }
+            y[c] = yy;
+            z[c] = zz;
+          }
+          float M = 0.0f;
+          if constexpr (SHIFT) {
+            M = y[0];
 #pragma unroll
             for (int c = 1; c < R; ++c) M = fmaxf(M, y[c]);
-            const float Dp = mu4[pp] - EF + gZ;
-            float ssum = 0.0f, ez = 0.0f, a1[V];
+          }
+          const float Dp = pmu - EFg;  // mu_{t-1} - E[F] + g_Z
+          float s = 0.0f, ez = 0.0f, ga[V];
 #pragma unroll
-            for (int v = 0; v < V; ++v) a1[v] = 0.0f;
+          for (int v = 0; v < V; ++v) ga[v] = 0.0f;
 #pragma unroll
-            for (int c = 0; c < R; ++c) {
-              const float e = fexp2(y[c] - M);
-              ssum += e;
-              const float ezc = e * z[c];
-              ez += ezc;
-              const float w = fmaf(e, Dp, ezc);  // e * (z + Dp)
+          for (int c = 0; c < R; ++c) {
+            const float e = fexp2(y[c] - M);
+            const float ezc = e * z[c];
+            s = c ? s + e : e;
+            ez = c ? ez + ezc : ezc;
+            const float wgt = fmaf(e, Dp, ezc);  // e * (z + Dp)
 #pragma unroll
-              for (int v = 0; v < V; ++v) a1[v] = fmaf(w, cc[c][v], a1[v]);
+            for (int v = 0; v < V; ++v) ga[v] = c ? fmaf(wgt, hh[c][v], ga[v]) : wgt * hh[c][v];
+          }
+          const float G = fexp2(pms + M);
+          a0 = G * fmaf(Dp, s, ez);
+#pragma unroll
+          for (int v = 0; v < V; ++v) a1[v] = G * ga[v];
+          no = flog2(s) + (M - oout);
+          nuo = ez * frcp(s);
+          return s;
+        };
+
+        auto read_in = [&](int i, float (&n)[R], float (&nu)[R]) {
+          const uint32_t yi = yb ^ Ku[i];
+#pragma unroll
+          for (int c = 0; c < R; ++c) {
+            if (t != N - 1) {
+              const float2 v2 = lds_pair(yi ^ koff(c));
+              n[c] = v2.x;
+              nu[c] = v2.y;
+            } else {
+              n[c] = 0.0f;
+              nu[c] = 0.0f;
             }
-            const float G = fexp2(M + m4[pp] + Kt);
-            A0 = fmaf(G, fmaf(Dp, ssum, ez), A0);
+          }
+        };
+        float nx[R], nxu[R];
+        read_in(0, nx, nxu);
+        float A0 = 0.0f, A1[V];
 #pragma unroll
-            for (int v = 0; v < V; ++v) A1[v] = fmaf(G, a1[v], A1[v]);
-            const float no = M + flog2(ssum);
-            mbuf[p * NB + u] = no;
-            mubuf[p * NB + u] = ez * frcp(ssum);
-            tmax = fmaxf(tmax, no);
+        for (int v = 0; v < V; ++v) A1[v] = 0.0f;
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+          const int q = tid + i * nthr;
+          // Consume the head of the slot pair and fetch the butterfly two ahead.
+          float pm[R], pmu[R], ni[R], nui[R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            pm[r] = pa[r];
+            pmu[r] = pua[r];
+            pa[r] = pb[r];
+            pua[r] = pub[r];
+            ni[r] = nx[r];
+            nui[r] = nxu[r];
+          }
+          if constexpr (kPair) {
+            const int tt = i + 2 < UPT ? t : t - 1 - (i + 2 - UPT) / UPT;
+            const int ii = i + 2 < UPT ? i + 2 : (i + 2 - UPT) % UPT;
+            if (tt >= 0) {
+              const float* src = slot_src(tt, ii);
+              load_vec<R>(src, pb);
+              load_vec<R>(src + R, pub);
+            }
+          }
+          if (i + 1 < UPT) read_in(i + 1, nx, nxu);
+          __builtin_amdgcn_sched_barrier(0);
+          if (q < NB) {
+            const int u = opaque(q);
+            float Mu = ni[0];
+#pragma unroll
+            for (int c = 1; c < R; ++c) Mu = fmaxf(Mu, ni[c]);
+            const float sh = -Mu;
+            float nr[R];
+#pragma unroll
+            for (int c = 0; c < R; ++c) nr[c] = ni[c] + sh;
+            const uint32_t xu = CT::A * (uint32_t)(R * u) + CT::B;
+            const float oout = sh + Qv;
+            const float kts = Kt - sh;
+            const uint32_t yi = yb ^ Ku[i];
+            if constexpr (kPair) {
+              float no[R], nuo[R], smin = 0.0f, ua0 = 0.0f, ua1[V];
+#pragma unroll
+              for (int v = 0; v < V; ++v) ua1[v] = 0.0f;
+#pragma unroll
+              for (int p = 0; p < R; ++p) {
+                float a0, a1[V];
+                const float s = beta_out(Fast{}, p, xu, u, nr, nui, pm[p] + kts, pmu[p], oout, no[p], nuo[p], a0, a1);
+                smin = p ? fminf(smin, s) : s;
+                ua0 += a0;
+#pragma unroll
+                for (int v = 0; v < V; ++v) ua1[v] += a1[v];
+              }
+              if constexpr (!EXACT) {
+                if (smin < kUnderflow) {
+                  ua0 = 0.0f;
+#pragma unroll
+                  for (int v = 0; v < V; ++v) ua1[v] = 0.0f;
+#pragma unroll
+                  for (int p = 0; p < R; ++p) {
+                    float a0, a1[V];
+                    beta_out(std::true_type{}, p, xu, u, nr, nui, pm[p] + kts, pmu[p], oout, no[p], nuo[p], a0, a1);
+                    ua0 += a0;
+#pragma unroll
+                    for (int v = 0; v < V; ++v) ua1[v] += a1[v];
+                  }
+                }
+              }
+              A0 += ua0;
+#pragma unroll
+              for (int v = 0; v < V; ++v) A1[v] += ua1[v];
+#pragma unroll
+              for (int p = 0; p < R; ++p) {
+                lds_pair(yi ^ koff(p)) = make_float2(no[p], nuo[p]);
+                tmax = fmaxf(tmax, no[p]);
+              }
+            } else {
+              const float* src = slot_src(t, i);
+#pragma unroll kOuterUnroll<R>
+              for (int p = 0; p < R; ++p) {
+                float no, nuo, a0, a1[V];
+                const float pms = src[p] + kts, pmup = src[R + p];
+                const float s = beta_out(Fast{}, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
+                if (!EXACT && s < kUnderflow)
+                  beta_out(std::true_type{}, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
+                A0 += a0;
+#pragma unroll
+                for (int v = 0; v < V; ++v) A1[v] += a1[v];
+                lds_pair(yi ^ koff(p)) = make_float2(no, nuo);
+                tmax = fmaxf(tmax, no);
+              }
+            }
           }
         }
-      }
-      D += (double)Qv;
-      A0 = wave_sum(A0);
-      if (lane == 0) apart[(t * nwaves + wave) * (V + 1)] = A0;
+        D += (double)Qv;
+        A0 = wave_sum(A0);
+        if (lane == 0) apart[(t * nwaves + wave) * (V + 1)] = A0;
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        const float s = wave_sum(A1[v]);
-        if (lane == 0) apart[(t * nwaves + wave) * (V + 1) + 1 + v] = s;
+        for (int v = 0; v < V; ++v) {
+          const float s = wave_sum(A1[v]);
+          if (lane == 0) apart[(t * nwaves + wave) * (V + 1) + 1 + v] = s * CT::kSigma;
+        }
+        tmax = wave_max(tmax);
+        if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
+        rho = rho - KV < 0 ? rho - KV + nb : rho - KV;
+        __syncthreads();
       }
-      tmax = wave_max(tmax);
-      if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
-      __syncthreads();
+    };
+    if (Tb < kExactBelowT) {
+      sweeps(std::true_type{});
+    } else {
+      sweeps(std::false_type{});
     }
 
     const float twoT = 2.0f / Tb;
@@ -318,16 +562,12 @@ const void* bwd_kernel_ptr(int KV, int V, int code, int upt) {
   BCJR_BWD_UPTS(2, 1, CODE_3INST)
   BCJR_BWD_UPTS(2, 2, CODE_TABLE)
   BCJR_BWD_UPTS(2, 2, CODE_HYB)
+  // kV = 4: whole 16-way butterflies, at most 256 per sequence (L <= 16).
   BCJR_BWD_CASE(4, 1, CODE_TABLE, 1)
-  BCJR_BWD_CASE(4, 1, CODE_TABLE, 2)
   BCJR_BWD_CASE(4, 1, CODE_1MAD, 1)
-  BCJR_BWD_CASE(4, 1, CODE_1MAD, 2)
   BCJR_BWD_CASE(4, 1, CODE_3INST, 1)
-  BCJR_BWD_CASE(4, 1, CODE_3INST, 2)
   BCJR_BWD_CASE(4, 2, CODE_TABLE, 1)
-  BCJR_BWD_CASE(4, 2, CODE_TABLE, 2)
   BCJR_BWD_CASE(4, 2, CODE_HYB, 1)
-  BCJR_BWD_CASE(4, 2, CODE_HYB, 2)
   return nullptr;
 }
 

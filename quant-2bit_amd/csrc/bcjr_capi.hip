@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <string>
 
@@ -72,6 +73,7 @@ struct Plan {
   size_t lds = 0;
   size_t slot_bytes = 0;
   int max_blocks = 0;  // resident blocks on the device
+  bcjr::Swizzle swz = {{31, 31, 31, 31}, {0, 0, 0, 0}};
 };
 
 int validate(const bcjr_problem* p) {
@@ -94,14 +96,14 @@ int validate(const bcjr_problem* p) {
       break;
     case BCJR_CODE_HYB:
       if (p->V != 2) return fail(BCJR_EINVAL, "HYB code is 2-D (V=2), got V=%d", p->V);
-      if (p->Q < 1 || p->Q > 12 || p->Q > 15) return fail(BCJR_EINVAL, "HYB Q=%d outside [1, 12]", p->Q);
+      if (p->Q < 1 || p->Q > 12) return fail(BCJR_EINVAL, "HYB Q=%d outside [1, 12]", p->Q);
       break;
     default: return fail(BCJR_EINVAL, "unknown code %d", p->code);
   }
   return BCJR_OK;
 }
 
-enum { OP_FWD = BCJR_OP_FORWARD, OP_BWD = BCJR_OP_BACKWARD, OP_VIT = BCJR_OP_VITERBI };
+enum { OP_FWD = BCJR_OP_FORWARD, OP_BWD = BCJR_OP_BACKWARD, OP_VIT = BCJR_OP_VITERBI, OP_FWD_INTERNALS = 3 };
 
 // Plans depend on (device, op, L, k, V, N, code, Q) only; they are cached so that
 // steady-state calls (and calls made while a stream is being captured into a
@@ -150,6 +152,88 @@ int make_plan(const bcjr_problem* p, int op, Plan* pl) {
   return BCJR_OK;
 }
 
+// LDS bank conflicts of the backward kernel's in-place layout: element
+// S(rotr(k*NB + u, rho)) holds slot k of butterfly u, one 8-byte (m~, mu) pair,
+// read and written by the same lane.  Measured on gfx950: a 64-bit LDS read
+// serves each 32-lane half of a wave from 32 eight-byte banks (conflict-free
+// when the half's elements differ mod 32); a 64-bit write serves 16 lanes at a
+// time from 32 four-byte banks (conflict-free when each quarter's elements
+// differ mod 16).  One wave of butterflies (u = 0..63) suffices: higher bits of
+// u XOR the same constant into every element of the wave.  Returns the extra
+// passes summed over the rotations a sweep reaches (multiples of gcd(kV, nb))
+// and the slots.
+int swizzle_cost(int L, int KV, const bcjr::Swizzle& s) {
+  const int nb = L - KV, NB = 1 << (nb - KV), R = 1 << KV;
+  const int lanes = std::min(NB, 64);
+  const uint32_t mask = (1u << nb) - 1u;
+  int g = KV, h = nb;
+  while (h) {
+    const int r = g % h;
+    g = h;
+    h = r;
+  }
+  int cost = 0;
+  uint32_t el[64];
+  for (int rho = 0; rho < nb; rho += g)
+    for (int k = 0; k < R; ++k) {
+      for (int l = 0; l < lanes; ++l) {
+        const uint32_t j = (uint32_t)(k * NB + l);
+        const uint32_t x = ((j | (j << nb)) >> rho) & mask;
+        uint32_t e = x;
+        for (int f = 0; f < 4; ++f) e ^= (x >> s.a[f]) & s.m[f];
+        el[l] = e;
+      }
+      for (int group = 16; group <= 32; group *= 2)  // writes: 16 mod 16; reads: 32 mod 32
+        for (int l0 = 0; l0 < lanes; l0 += group) {
+          int cnt[32] = {0}, worst = 0;
+          for (int l = l0; l < std::min(lanes, l0 + group); ++l) worst = std::max(worst, ++cnt[el[l] % group]);
+          cost += worst - 1;
+        }
+    }
+  return cost;
+}
+
+// Cheapest swizzle: up to four fields of 4 or 5 bits at shifts >= their width,
+// taken in order of increasing count and kept only when strictly better; the
+// search stops at the first conflict-free layout.
+bcjr::Swizzle pick_swizzle(int L, int KV) {
+  const int nb = L - KV;
+  bcjr::Swizzle best = {{31, 31, 31, 31}, {0, 0, 0, 0}};
+  int best_cost = swizzle_cost(L, KV, best);
+  for (int nf = 1; nf <= 4 && best_cost > 0; ++nf) {
+    int sh[4];
+    // shifts sh[0] < ... < sh[nf-1] in [4, nb), widths from the bits of wbits
+    std::function<void(int, int)> rec = [&](int f, int lo) {
+      if (best_cost == 0) return;
+      if (f == nf) {
+        for (int wbits = 0; wbits < (1 << nf) && best_cost > 0; ++wbits) {
+          bcjr::Swizzle s = {{31, 31, 31, 31}, {0, 0, 0, 0}};
+          bool ok = true;
+          for (int i = 0; i < nf; ++i) {
+            const int w = 4 + ((wbits >> i) & 1);
+            if (sh[i] < w) ok = false;
+            s.a[i] = sh[i];
+            s.m[i] = (1u << w) - 1u;
+          }
+          if (!ok) continue;
+          const int cost = swizzle_cost(L, KV, s);
+          if (cost < best_cost) {
+            best_cost = cost;
+            best = s;
+          }
+        }
+        return;
+      }
+      for (int a = lo; a < nb; ++a) {
+        sh[f] = a;
+        rec(f + 1, a + 1);
+      }
+    };
+    rec(0, 4);
+  }
+  return best;
+}
+
 int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan* pl) {
   const int KV = p->k * p->V, R = 1 << KV, RO = R < 4 ? R : 4;
   pl->KV = KV;
@@ -157,6 +241,7 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
   pl->NSUB = R / RO;
   pl->NT = 1 << (p->L - KV);
   pl->NB = pl->NT >> KV;
+  if (op != OP_VIT) pl->NSUB = 1;  // the soft kernels take whole butterflies per unit
   pl->NU = pl->NB * pl->NSUB;
   const int max_thr = 512;
   int nthr = ((pl->NU + 63) / 64) * 64;
@@ -168,15 +253,23 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
   pl->upt = upt;
   const int nwaves = nthr / 64;
   const int N = (int)p->N;
-  if (op == OP_FWD || op == OP_VIT) {
-    pl->cache = (pl->NSUB == 1) && (upt * R * R * p->V <= 128);
-    pl->fn = (op == OP_FWD) ? bcjr::fwd_kernel_ptr(KV, p->V, p->code, upt, pl->cache)
-                            : bcjr::vit_kernel_ptr(KV, p->V, p->code, upt, pl->cache);
-    pl->lds = (op == OP_FWD) ? bcjr::fwd_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q)
-                             : bcjr::vit_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q);
-    pl->slot_bytes = (op == OP_FWD) ? (size_t)N * pl->NT * sizeof(float) : (size_t)N * pl->NT;
+  if (op == OP_FWD || op == OP_FWD_INTERNALS || op == OP_VIT) {
+    const bool fwd = (op != OP_VIT);
+    // Codeword cache in VGPRs: up to 128 per thread for tables and the
+    // Viterbi kernel; the soft forward keeps hash codes in registers only up to
+    // 64 (at 8 butterflies per thread the cache would spill, and a hash costs
+    // three VALU per state).
+    const bool hash = p->code == BCJR_CODE_1MAD || p->code == BCJR_CODE_3INST;
+    const int cache_max = (fwd && hash) ? 64 : 128;
+    pl->cache = (pl->NSUB == 1) && (upt * R * R * p->V <= cache_max);
+    pl->fn = fwd ? bcjr::fwd_kernel_ptr(KV, p->V, p->code, upt, pl->cache, op == OP_FWD_INTERNALS)
+                 : bcjr::vit_kernel_ptr(KV, p->V, p->code, upt, pl->cache);
+    pl->lds = fwd ? bcjr::fwd_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q)
+                  : bcjr::vit_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q);
+    pl->slot_bytes = fwd ? (size_t)N * pl->NT * sizeof(float) : (size_t)N * pl->NT;
   } else {
     pl->cache = false;
+    pl->swz = pick_swizzle(p->L, KV);
     pl->fn = bcjr::bwd_kernel_ptr(KV, p->V, p->code, upt);
     pl->lds = bcjr::bwd_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q);
     pl->slot_bytes = (size_t)N * 2 * pl->NT * sizeof(float);
@@ -256,7 +349,7 @@ int bcjr_forward_internals(const bcjr_problem* prob, const float* seq, const flo
                            const float* codebook_or_lut, float* soft, float* logZ, float* marginals,
                            float* log_alpha, float* log_beta, void* ws, size_t ws_bytes, hipStream_t stream) {
   Plan pl;
-  int rc = make_plan(prob, OP_FWD, &pl);
+  int rc = make_plan(prob, OP_FWD_INTERNALS, &pl);
   if (rc) return rc;
   if (prob->B == 0) return BCJR_OK;
   if (!seq || !T || !soft || !ws || !marginals || !log_alpha || !log_beta)
@@ -306,6 +399,7 @@ int bcjr_backward(const bcjr_problem* prob, const float* seq, const float* T, co
   P.L = prob->L;
   P.Q = prob->Q;
   P.t_per_seq = prob->t_per_seq ? 1 : 0;
+  P.swz = pl.swz;
   return launch(pl, prob->B, ws_bytes, &P, stream);
 }
 

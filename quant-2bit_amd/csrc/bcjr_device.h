@@ -20,6 +20,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 namespace bcjr {
@@ -38,8 +40,7 @@ __device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x)
 // Codeword generators.  The "exact" forms are bit-identical to the reference
 // (src/codes/ref.py:33-41 for 1MAD, :76-91 for 3INST, src/qat/ste.py:376-392 for
 // HYB); they are used wherever a codeword is computed once and cached, and by
-// the Viterbi path.  code_1mad_fast trades the correctly-rounded division for a
-// multiply by the reciprocal (<= 1 ulp), for per-cell use in the soft kernels.
+// the Viterbi path.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int mad1_bytesum_centered(uint32_t s) {
   const uint32_t x = 34038481u * s + 76625530u;
@@ -49,10 +50,6 @@ __device__ __forceinline__ int mad1_bytesum_centered(uint32_t s) {
 
 __device__ __forceinline__ float code_1mad_exact(uint32_t s) {
   return __fdiv_rn((float)mad1_bytesum_centered(s), 147.8f);
-}
-
-__device__ __forceinline__ float code_1mad_fast(uint32_t s) {
-  return (float)mad1_bytesum_centered(s) * (1.0f / 147.8f);
 }
 
 __device__ __forceinline__ float code_3inst(uint32_t s) {
@@ -75,7 +72,7 @@ __device__ __forceinline__ void code_hyb(uint32_t s, const float* lut, int Q, fl
 
 // c(s) for the soft kernels.  `table` is the global (S, V) codebook for
 // CODE_TABLE; `lut` the LDS copy of the HYB LUT.
-template <int CODE, int V, bool EXACT>
+template <int CODE, int V>
 __device__ __forceinline__ void codeword(uint32_t s, const float* __restrict__ table,
                                          const float* lut, int Q, float (&c)[V]) {
   if constexpr (CODE == CODE_TABLE) {
@@ -87,7 +84,7 @@ __device__ __forceinline__ void codeword(uint32_t s, const float* __restrict__ t
     }
   } else if constexpr (CODE == CODE_1MAD) {
     static_assert(V == 1, "1MAD is a scalar code");
-    c[0] = EXACT ? code_1mad_exact(s) : code_1mad_fast(s);
+    c[0] = code_1mad_exact(s);
   } else if constexpr (CODE == CODE_3INST) {
     static_assert(V == 1, "3INST is a scalar code");
     c[0] = code_3inst(s);
@@ -97,12 +94,128 @@ __device__ __forceinline__ void codeword(uint32_t s, const float* __restrict__ t
   }
 }
 
+// ---------------------------------------------------------------------------
+// Raw codewords for the soft kernels: c(s) = kSigma * h(s) with h cheap to form.
+// The LCG codes hash x(s) = A*s + B; for the butterfly states
+// s = p*NT + R*u + c this is x = (A*R*u + B) + A*(p*NT + c): one integer add per
+// state on top of a per-butterfly base.  h is exact:
+//   1MAD : h = (byte sum of x) - 510   (v_sad_u8 with the -510 in its accumulator)
+//   3INST: h = f16(lo) + f16(hi)       (one v_dot2 with (1, 1); the sum is exact)
+// Tables and HYB have kSigma = 1 and h = c.
+// ---------------------------------------------------------------------------
+template <int CODE> struct CodeTraits {
+  static constexpr uint32_t A = 0, B = 0;
+  static constexpr float kSigma = 1.0f;
+};
+template <> struct CodeTraits<CODE_1MAD> {
+  static constexpr uint32_t A = 34038481u, B = 76625530u;
+  static constexpr float kSigma = 1.0f / 147.8f;
+};
+template <> struct CodeTraits<CODE_3INST> {
+  static constexpr uint32_t A = 89226354u, B = 64248484u;
+  static constexpr float kSigma = (float)(1.0 / 1.2447);
+};
+
+typedef _Float16 bcjr_half2 __attribute__((ext_vector_type(2)));
+
+template <int CODE>
+__device__ __forceinline__ float raw_from_hash(uint32_t x) {
+  if constexpr (CODE == CODE_1MAD) {
+    return (float)(int)__builtin_amdgcn_sad_u8(x, 0u, (uint32_t)-510);
+  } else {
+    const uint32_t y = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+    const bcjr_half2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(bcjr_half2, y), one, 0.0f, false);
+  }
+}
+
+// d = h * ssk + nw for the 3INST code straight from the hash: h is the sum of
+// the two f16 halves of y, so d = fma(lo, ssk, fma(hi, ssk, nw)) with f16
+// sources, which the compiler forms as two v_fma_mix_f32 (no f32 h is needed).
+// Two roundings instead of one: |error| <= 2 ulp(d).
+__device__ __forceinline__ float d_3inst(uint32_t x, float ssk, float nw) {
+  const uint32_t y = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+  const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(y & 0xFFFFu));
+  const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(y >> 16));
+  return fmaf((float)lo, ssk, fmaf((float)hi, ssk, nw));
+}
+
+// h(s) for state s = p*NT + R*u + c given the per-butterfly hash base
+// xu = A*(R*u) + B (LCG codes) or the state index s (tables).
+template <int CODE, int V>
+__device__ __forceinline__ void raw_codeword(uint32_t xu, uint32_t off, uint32_t s,
+                                             const float* __restrict__ table, const float* lut, int Q,
+                                             float (&h)[V]) {
+  if constexpr (CODE == CODE_1MAD || CODE == CODE_3INST) {
+    h[0] = raw_from_hash<CODE>(xu + off);
+  } else if constexpr (CODE == CODE_TABLE) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) h[v] = table[(size_t)s * V + v];
+  } else {
+    code_hyb(s, lut, Q, h[0], h[1]);
+  }
+}
+
+// Group log-sum-exp.  The R inputs of a butterfly are normalised by their
+// maximum, so every term 2^a of a group is <= 1 and, at moderate temperature,
+// the group sum needs no per-group maximum: one exp2 per term, no compare or
+// subtract.  A butterfly with a group sum below kUnderflow (every term of the
+// group < -120) is recomputed against the group maxima (exec-masked, rare for
+// T >= kExactBelowT).  Below kExactBelowT that fallback would fire in most
+// waves, so sequences with a lower temperature use the group maxima throughout.
+constexpr float kUnderflow = 0x1p-120f;
+constexpr float kExactBelowT = 0.08f;
+
+// Load / store n consecutive floats (16-byte aligned when n % 4 == 0, 8-byte
+// aligned when n == 2).
+template <int n>
+__device__ __forceinline__ void load_vec(const float* src, float* dst) {
+  if constexpr (n % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < n; i += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(src + i);
+      dst[i] = v.x;
+      dst[i + 1] = v.y;
+      dst[i + 2] = v.z;
+      dst[i + 3] = v.w;
+    }
+  } else if constexpr (n == 2) {
+    const float2 v = *reinterpret_cast<const float2*>(src);
+    dst[0] = v.x;
+    dst[1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < n; ++i) dst[i] = src[i];
+  }
+}
+
+template <int n>
+__device__ __forceinline__ void store_vec(float* dst, const float* src) {
+  if constexpr (n % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < n; i += 4)
+      *reinterpret_cast<float4*>(dst + i) = make_float4(src[i], src[i + 1], src[i + 2], src[i + 3]);
+  } else if constexpr (n == 2) {
+    *reinterpret_cast<float2*>(dst) = make_float2(src[0], src[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < n; ++i) dst[i] = src[i];
+  }
+}
+
 // Returns x unchanged but opaque to the optimiser.  Kernels that recompute
 // codewords every step pass their butterfly index through this inside the step
 // loop; otherwise loop-invariant code motion hoists all R*R codewords per unit
 // out of the N-step loop and the kernel spills.
 __device__ __forceinline__ int opaque(int x) {
   asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Wave-uniform variant.  The LCG kernels keep A*NT behind it so that
+// base + A*(p*NT + c) cannot be refolded into one multiply A*s + B per state.
+__device__ __forceinline__ uint32_t opaque_uniform(uint32_t x) {
+  asm volatile("" : "+s"(x));
   return x;
 }
 
@@ -139,6 +252,29 @@ struct FwdParams {
   int N, L, Q, t_per_seq;
 };
 
+// In-place layout of a reduced-state vector in LDS.  Reduced state j of the
+// vector after step t sits at element S(rotr(j, rho_t)), rotr over nb = L - kV
+// bits and rho_t = kV * (t - 1) mod nb.  Because rotr(R*u + r, kV) = r*NB + u,
+// the R inputs of butterfly u at step t and its R outputs occupy the same R
+// elements, so each thread updates its butterflies in place with one barrier
+// per step.  S XORs up to four higher bit fields (x >> a[i]) & m[i] into the low
+// bits (a shift of 31 drops a field); the host picks the fields that keep every
+// rotation free of LDS bank conflicts.  S is linear: S(x ^ y) = S(x) ^ S(y).
+struct Swizzle {
+  int a[4];
+  uint32_t m[4];
+};
+
+__device__ __forceinline__ uint32_t swizzle(uint32_t x, const Swizzle& s) {
+  return x ^ ((x >> s.a[0]) & s.m[0]) ^ ((x >> s.a[1]) & s.m[1]) ^ ((x >> s.a[2]) & s.m[2]) ^
+         ((x >> s.a[3]) & s.m[3]);
+}
+
+// rotr of an nb-bit value (nb <= 16).
+__device__ __forceinline__ uint32_t rotr_bits(uint32_t x, int rho, int nb) {
+  return ((x | (x << nb)) >> rho) & ((1u << nb) - 1u);
+}
+
 struct BwdParams {
   const float* seq;
   const float* T;
@@ -149,6 +285,7 @@ struct BwdParams {
   float* ws;            // slots x (N * 2 * NT) floats
   long long B;
   int N, L, Q, t_per_seq;
+  Swizzle swz;          // LDS layout of (m~, mu) and (n~, nu)
 };
 
 struct VitParams {

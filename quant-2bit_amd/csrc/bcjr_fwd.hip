@@ -4,53 +4,60 @@
 // and the forward of BcjrForwardBackwardMonolithic (src/bcjr/bcjr_monolithic.py:161-189).
 //
 // One workgroup processes one sequence at a time (grid-stride over sequences) and
-// owns one scratch slot of N * NT floats in HBM.
+// owns one scratch slot of N * NT floats in HBM.  All log values are base 2.
 //
-// Alpha sweep (t = 0..N-1), butterfly u of step t:
-//   mi[p]  = m~_{t-1}(p*NB + u) - O_t            (O_t: max of m~_{t-1}, from the
-//                                                  per-wave maxima of step t-1)
-//   a[p][r] = mi[p] + ll2_t(p*NT + R*u + r)
-//   m~_t(R*u + r) = LSE2_p a[p][r]                 (exact per-group max, exp2/log2)
-//   The butterfly's normalised inputs mi[0..R-1] are also written, as one
-//   contiguous R-float vector, to slot[t][u]: exactly what the beta sweep needs.
-//   True log-alpha: alpha2_t(s) = ll2_t(s) + mi[p] + C_t with C_t = sum_{tau<=t} O_tau.
+// Alpha sweep (t = 0..N-1), butterfly u of step t, raw inputs m[p] = m~_{t-1}(p*NB + u)
+// (true m_{t-1} = m~_{t-1} + C_{t-1}):
+//   sh = -max_p m[p];   a[p][r] = m[p] + sh + ll2_t(p*NT + R*u + r)  (<= 0)
+//   m~_t(R*u + r) = log2(sum_p 2^a[p][r]) - sh - O_t   (group sum, zero shift)
+//   where O_t = max_j m~_{t-1}(j) (block-uniform, from the per-wave maxima) keeps
+//   values O(1), and C_t = C_{t-1} + O_t.  One exp2 per state; one log2 per group.
+//   The raw inputs m[0..R-1] go to slot[t][u] (R contiguous floats): exactly
+//   what the beta sweep needs at step t.
 // log2 Z = C_{N-1} + LSE2_j m~_{N-1}(j).
-// Beta sweep (t = N-1..0), same butterfly (transposed data flow):
-//   ni[c] = n~_t(R*u + c) - Q_t,  y[p][c] = ni[c] + ll2_t(p*NT + R*u + c),
-//   n~_{t-1}(p*NB + u) = M_p + log2(sum_c 2^(y - M_p)),
-//   P_t(s) = 2^(y + mi[p] + K_t) with K_t = C_t + Q_t + D_t - log2 Z (D_t: beta offsets),
-//   so the marginal costs one multiply per state and one exp2 per group:
-//   P = e[p][c] * 2^(M_p + mi[p] + K_t).  soft_t = sum_s P_t(s) c(s).
-// Both sweeps normalise by a block-uniform offset every step, so all values stay
-// O(1)-O(100) in float32; offsets accumulate in double.
+// Beta sweep (t = N-1..0), same butterfly with the transposed data flow, raw
+// inputs n[c] = n~_t(R*u + c) (true n_t = n~_t + D_t):
+//   sh = -max_c n[c];  y[p][c] = n[c] + sh + ll2_t(p*NT + R*u + c)
+//   e = 2^y,  n~_{t-1}(p*NB + u) = log2(sum_c e) - sh - Q_t,  D_{t-1} = D_t + Q_t
+//   P_t(s) = e * 2^(m[p] - sh + K_t),  K_t = C_{t-1} + D_t - log2 Z,
+//   so a marginal costs one multiply per state and one exp2 per group, and
+//   soft_t = sum_s P_t(s) c(s) accumulates per thread, then per wave.
+// Offsets accumulate in double on every thread (they are block-uniform).
+//
+// Group sums take the zero-shift form (the inputs are normalised by the
+// butterfly maximum, so each term is <= 1 and needs no group maximum); a
+// butterfly with any underflowed group (sum < kUnderflow) is recomputed against
+// the group maxima, rare at T >= kExactBelowT; below it every group uses them.
+// A unit is one whole butterfly: R inputs, R outputs, R*R states.
 #include "bcjr_device.h"
 #include "bcjr_kernels.h"
 
 namespace bcjr {
 
-template <int KV, int V, int CODE, int UPT, bool CACHE>
+template <int KV, int V, int CODE, int UPT, bool CACHE, bool INTERNALS>
 __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   constexpr int R = 1 << KV;
-  constexpr int RO = R < 4 ? R : 4;  // outputs per unit
-  constexpr int NSUB = R / RO;       // units per butterfly
-  static_assert(!CACHE || NSUB == 1, "codeword cache needs whole butterflies per thread");
+  // Butterflies of 2 or 4 states run fully unrolled with their slot inputs
+  // prefetched in registers; 16-state butterflies loop over outputs.
+  constexpr bool kPair = R <= 4;
+  static_assert(!CACHE || kPair, "codeword cache is for butterflies of at most 4 states");
+  using CT = CodeTraits<CODE>;
 
   extern __shared__ __align__(16) unsigned char smem[];
   const int L = P.L, N = P.N;
   const int NT = 1 << (L - KV);
   const int NB = NT >> KV;
-  const int NU = NB * NSUB;
-  const int lgNB = L - 2 * KV;
+  const uint32_t ANT = opaque_uniform(CT::A * (uint32_t)NT);  // hash offset of p * NT
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
 
-  double* cvec = reinterpret_cast<double*>(smem);  // N    C_t
-  float* mbuf = reinterpret_cast<float*>(cvec + N);  // 2*NT reduced state, double-buffered
-  float* wmax = mbuf + 2 * NT;                       // 2*kMaxWaves
-  float* wsum = wmax + 2 * kMaxWaves;                // kMaxWaves
-  float* wbuf = wsum + kMaxWaves;                    // N*V   sequence
-  float* spart = wbuf + N * V;                       // N*nwaves*V per-wave soft partials
-  float* lut = spart + N * nwaves * V;               // HYB LUT
+  double* cvec = reinterpret_cast<double*>(smem);                // N    C_{t-1}
+  float* mbuf = reinterpret_cast<float*>(cvec + ((N + 1) & ~1));  // 2*NT reduced state (16-B aligned)
+  float* wmax = mbuf + 2 * NT;                                    // 2*kMaxWaves
+  float* wsum = wmax + 2 * kMaxWaves;                             // kMaxWaves
+  float* wbuf = wsum + kMaxWaves;                                 // N*V   sequence
+  float* spart = wbuf + N * V;                                    // N*nwaves*V per-wave soft partials
+  float* lut = spart + N * nwaves * V;                            // HYB LUT
 
   if constexpr (CODE == CODE_HYB) {
     const int nl = 2 << P.Q;
@@ -58,16 +65,20 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
     __syncthreads();
   }
 
-  float cw[CACHE ? UPT : 1][CACHE ? R : 1][CACHE ? R : 1][V];
+  // Raw codewords h of this thread's butterflies, fixed for the whole launch.
+  float hc[CACHE ? UPT : 1][CACHE ? R : 1][CACHE ? R : 1][V];
   if constexpr (CACHE) {
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
-      const int u = min(tid + i * nthr, NU - 1);
+      const int u = min(tid + i * nthr, NB - 1);
+      const uint32_t xu = CT::A * (uint32_t)(R * u) + CT::B;
 #pragma unroll
       for (int p = 0; p < R; ++p)
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-          codeword<CODE, V, true>((uint32_t)(p * NT + R * u + r), P.table, lut, P.Q, cw[i][p][r]);
+        for (int r = 0; r < R; ++r) {
+          const uint32_t s = (uint32_t)(p * NT + R * u + r);
+          raw_codeword<CODE, V>(xu, CT::A * (uint32_t)(p * NT + r), s, P.table, lut, P.Q, hc[i][p][r]);
+        }
     }
   }
 
@@ -75,193 +86,333 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
     float* slot = P.ws + (size_t)blockIdx.x * (size_t)N * (size_t)NT;
     const float Tb = P.T[P.t_per_seq ? b : 0];
     const float sk = sqrtf(kLog2e / Tb);
+    const float ssk = CT::kSigma * sk;  // d = (c - w) * sk = h * ssk - w * sk
     const float* seqb = P.seq + (size_t)b * N * V;
     for (int i = tid; i < N * V; i += nthr) wbuf[i] = seqb[i];
     __syncthreads();
 
-    // ------------------------------ alpha sweep ------------------------------
-    double C = 0.0;
-    int k = 0;  // step counter across both sweeps: LDS buffer / wmax parity
-    for (int t = 0; t < N; ++t, ++k) {
-      const float* prev = mbuf + ((k + 1) & 1) * NT;
-      float* cur = mbuf + (k & 1) * NT;
-      float O = (float)KV;  // m~_{-1} = log2(R) for every j
-      if (t > 0) {
-        O = -INFINITY;
-        for (int w = 0; w < nwaves; ++w) O = fmaxf(O, wmax[((k + 1) & 1) * kMaxWaves + w]);
-      }
-      C += (double)O;
-      if (tid == 0) cvec[t] = C;
-      float nw[V];
+    double logZ2 = 0.0;
+    // Below kExactBelowT most groups would underflow the zero-shift sums, so
+    // the whole sequence uses the group maxima.  The choice is a uniform branch
+    // around both sweeps: each variant gets its own register allocation.
+    auto sweeps = [&](auto exact_tag) {
+      constexpr bool EXACT = decltype(exact_tag)::value;
+      using Fast = std::integral_constant<bool, EXACT>;
+
+      // ------------------------------ alpha sweep ------------------------------
+      double C = 0.0;  // C_{t-1}
+      int k = 0;       // step counter across both sweeps: LDS buffer / wmax parity
+      for (int t = 0; t < N; ++t, ++k) {
+        const float* prev = mbuf + ((k + 1) & 1) * NT;
+        float* cur = mbuf + (k & 1) * NT;
+        float O = (float)KV;  // m~_{-1} = log2(R) for every j
+        if (t > 0) {
+          O = -INFINITY;
+          for (int w = 0; w < nwaves; ++w) O = fmaxf(O, wmax[((k + 1) & 1) * kMaxWaves + w]);
+        }
+        if (tid == 0) cvec[t] = C;
+        C += (double)O;
+        float nw[V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) nw[v] = -wbuf[t * V + v] * sk;
-      float tmax = -INFINITY;
+        for (int v = 0; v < V; ++v) nw[v] = -wbuf[t * V + v] * sk;
+
+        // Output r of butterfly u (unit i) from the shifted inputs m[p]
+        // (maximum 0): returns the group sum, mo = m~_t(R*u + r).
+        auto alpha_out = [&](auto shift_tag, int i, int r, uint32_t xu, int u, const float (&m)[R], float oout,
+                             float& mo) -> float {
+          constexpr bool SHIFT = decltype(shift_tag)::value;
+          float a[R];
 #pragma unroll
-      for (int i = 0; i < UPT; ++i) {
-        const int q = tid + i * nthr;
-        __builtin_amdgcn_sched_barrier(0);
-        if (q < NU) {
-          const int u = (CACHE ? q : opaque(q)) & (NB - 1);
-          const int sub = q >> lgNB;
-          float mi[R];
-#pragma unroll
-          for (int p = 0; p < R; ++p) mi[p] = t ? prev[p * NB + u] - O : 0.0f;
-          if (sub == 0) {
-            float* dst = slot + ((size_t)t * NB + u) * R;
-#pragma unroll
-            for (int p = 0; p < R; ++p) dst[p] = mi[p];
-          }
-          float mo[RO];
-#pragma unroll
-          for (int r = 0; r < RO; ++r) {
-            const int rr = sub * RO + r;
-            float a[R];
-#pragma unroll
-            for (int p = 0; p < R; ++p) {
-              float c[V];
+          for (int p = 0; p < R; ++p) {
+            float acc = m[p];
+            // The two-rounding d_3inst form is kept out of the low-temperature
+            // variant, where |d| reaches ~1e2 and float32 precision is tightest.
+            if constexpr (!CACHE && CODE == CODE_3INST && !EXACT) {
+              const float d = d_3inst(xu + p * ANT + CT::A * (uint32_t)r, ssk, nw[0]);
+              acc = fmaf(-d, d, acc);
+            } else {
+              float h[V];
               if constexpr (CACHE) {
 #pragma unroll
-                for (int v = 0; v < V; ++v) c[v] = cw[i][p][r][v];
+                for (int v = 0; v < V; ++v) h[v] = hc[i][p][r][v];
               } else {
-                codeword<CODE, V, false>((uint32_t)(p * NT + R * u + rr), P.table, lut, P.Q, c);
+                raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)r, (uint32_t)(p * NT + R * u + r), P.table,
+                                      lut, P.Q, h);
               }
-              float acc = mi[p];
 #pragma unroll
               for (int v = 0; v < V; ++v) {
-                const float d = fmaf(c[v], sk, nw[v]);
+                const float d = fmaf(h[v], ssk, nw[v]);
                 acc = fmaf(-d, d, acc);
               }
-              a[p] = acc;
             }
-            float M = a[0];
+            a[p] = acc;
+          }
+          float M = 0.0f;
+          if constexpr (SHIFT) {
+            M = a[0];
 #pragma unroll
             for (int p = 1; p < R; ++p) M = fmaxf(M, a[p]);
-            float ssum = 0.0f;
-#pragma unroll
-            for (int p = 0; p < R; ++p) ssum += fexp2(a[p] - M);
-            mo[r] = M + flog2(ssum);
-            tmax = fmaxf(tmax, mo[r]);
           }
-          float* o = cur + R * u + sub * RO;
+          float s = fexp2(a[0] - M);
 #pragma unroll
-          for (int r = 0; r < RO; ++r) o[r] = mo[r];
+          for (int p = 1; p < R; ++p) s += fexp2(a[p] - M);
+          mo = flog2(s) + (M - oout);
+          return s;
+        };
+
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+          const int q = tid + i * nthr;
+          __builtin_amdgcn_sched_barrier(0);
+          if (q < NB) {
+            const int u = CACHE ? q : opaque(q);
+            float m[R];
+#pragma unroll
+            for (int p = 0; p < R; ++p) m[p] = t ? prev[p * NB + u] : (float)KV;
+            store_vec<R>(slot + ((size_t)t * NB + u) * R, m);
+            float Mu = m[0];
+#pragma unroll
+            for (int p = 1; p < R; ++p) Mu = fmaxf(Mu, m[p]);
+            const float sh = -Mu;
+#pragma unroll
+            for (int p = 0; p < R; ++p) m[p] += sh;
+            const uint32_t xu = CT::A * (uint32_t)(R * u) + CT::B;
+            const float oout = sh + O;
+            if constexpr (kPair) {
+              float mo[R], smin = 0.0f;
+#pragma unroll
+              for (int r = 0; r < R; ++r) {
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo[r]);
+                smin = r ? fminf(smin, s) : s;
+              }
+              if constexpr (!EXACT) {
+                if (smin < kUnderflow) {
+#pragma unroll
+                  for (int r = 0; r < R; ++r) alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo[r]);
+                }
+              }
+              store_vec<R>(cur + R * u, mo);
+#pragma unroll
+              for (int r = 0; r < R; ++r) tmax = fmaxf(tmax, mo[r]);
+            } else {
+#pragma unroll 1
+              for (int r = 0; r < R; ++r) {
+                float mo;
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo);
+                if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo);
+                cur[R * u + r] = mo;
+                tmax = fmaxf(tmax, mo);
+              }
+            }
+          }
         }
+        tmax = wave_max(tmax);
+        if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
+        __syncthreads();
       }
-      tmax = wave_max(tmax);
-      if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
+
+      // log2 Z = C_{N-1} + LSE2 over the final reduced state.
+      const float* fin = mbuf + ((k + 1) & 1) * NT;
+      float Mz = -INFINITY;
+      for (int w = 0; w < nwaves; ++w) Mz = fmaxf(Mz, wmax[((k + 1) & 1) * kMaxWaves + w]);
+      float part = 0.0f;
+      for (int j = tid; j < NT; j += nthr) part += fexp2(fin[j] - Mz);
+      part = wave_sum(part);
+      if (lane == 0) wsum[wave] = part;
       __syncthreads();
-    }
+      float Ssum = 0.0f;
+      for (int w = 0; w < nwaves; ++w) Ssum += wsum[w];
+      logZ2 = C + (double)Mz + (double)flog2(Ssum);
 
-    // log2 Z = C_{N-1} + LSE2 over the final reduced state.
-    const float* fin = mbuf + ((k + 1) & 1) * NT;
-    float Mz = -INFINITY;
-    for (int w = 0; w < nwaves; ++w) Mz = fmaxf(Mz, wmax[((k + 1) & 1) * kMaxWaves + w]);
-    float part = 0.0f;
-    for (int j = tid; j < NT; j += nthr) part += fexp2(fin[j] - Mz);
-    part = wave_sum(part);
-    if (lane == 0) wsum[wave] = part;
-    __syncthreads();
-    float Ssum = 0.0f;
-    for (int w = 0; w < nwaves; ++w) Ssum += wsum[w];
-    const double logZ2 = C + (double)Mz + (double)flog2(Ssum);
+      // ------------------------------ beta sweep -------------------------------
+      // Raw alpha inputs of step t come back from HBM two butterflies ahead of
+      // their use, across step boundaries.
+      auto slot_src = [&](int t, int i) {
+        const int q = min(tid + i * nthr, NB - 1);
+        return slot + ((size_t)t * NB + q) * R;
+      };
+      float pa[R], pb[R];  // the next two butterflies in consumption order (t descending, i ascending)
+      if (kPair) load_vec<R>(slot_src(N - 1, 0), pa);
+      if (kPair && (UPT > 1 || N > 1)) load_vec<R>(UPT > 1 ? slot_src(N - 1, 1) : slot_src(N - 2, 0), pb);
+      double D = 0.0;  // D_t
+      for (int t = N - 1; t >= 0; --t, ++k) {
+        const float* prev = mbuf + ((k + 1) & 1) * NT;
+        float* cur = mbuf + (k & 1) * NT;
+        float Qv = 0.0f;
+        if (t != N - 1) {
+          Qv = -INFINITY;
+          for (int w = 0; w < nwaves; ++w) Qv = fmaxf(Qv, wmax[((k + 1) & 1) * kMaxWaves + w]);
+        }
+        const float Kt = (float)(cvec[t] + D - logZ2);
+        float nw[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) nw[v] = -wbuf[t * V + v] * sk;
 
-    // ------------------------------ beta sweep -------------------------------
-    double D = 0.0;
-    for (int t = N - 1; t >= 0; --t, ++k) {
-      const float* prev = mbuf + ((k + 1) & 1) * NT;
-      float* cur = mbuf + (k & 1) * NT;
-      float Qv = 0.0f;
-      if (t != N - 1) {
-        Qv = -INFINITY;
-        for (int w = 0; w < nwaves; ++w) Qv = fmaxf(Qv, wmax[((k + 1) & 1) * kMaxWaves + w]);
-      }
-      const float Kt = (float)(cvec[t] + (double)Qv + D - logZ2);
-      float nw[V];
+        // Output p of butterfly u (unit i) from the shifted inputs nr[c]
+        // (maximum 0): no = n~_{t-1}(p*NB + u) and the soft contribution
+        // G * sum_c e_c h_c, with pms = raw m~_{t-1}(p*NB + u) + K_t - sh.
+        // n holds the raw inputs and pmr the raw m~ (diagnostics only).
+        auto beta_out = [&](auto shift_tag, int i, int p, uint32_t xu, int u, const float (&nr)[R],
+                            const float (&n)[R], float pms, float pmr, float oout, float& no,
+                            float (&cs)[V]) -> float {
+          constexpr bool SHIFT = decltype(shift_tag)::value;
+          float y[R], hh[R][V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) nw[v] = -wbuf[t * V + v] * sk;
-      float acc[V];
+          for (int c = 0; c < R; ++c) {
+            if constexpr (CACHE) {
 #pragma unroll
-      for (int v = 0; v < V; ++v) acc[v] = 0.0f;
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < UPT; ++i) {
-        const int q = tid + i * nthr;
-        __builtin_amdgcn_sched_barrier(0);
-        if (q < NU) {
-          const int u = (CACHE ? q : opaque(q)) & (NB - 1);
-          const int sub = q >> lgNB;
-          float ni[R];
-#pragma unroll
-          for (int c = 0; c < R; ++c) ni[c] = (t != N - 1) ? prev[R * u + c] - Qv : 0.0f;
-          const float* src = slot + ((size_t)t * NB + u) * R + sub * RO;
-          float mi[RO];
-#pragma unroll
-          for (int pp = 0; pp < RO; ++pp) mi[pp] = src[pp];
-#pragma unroll
-          for (int pp = 0; pp < RO; ++pp) {
-            const int p = sub * RO + pp;
-            float y[R];
-            float cc[R][V];
-#pragma unroll
-            for (int c = 0; c < R; ++c) {
-              if constexpr (CACHE) {
-#pragma unroll
-                for (int v = 0; v < V; ++v) cc[c][v] = cw[i][pp][c][v];
-              } else {
-                codeword<CODE, V, false>((uint32_t)(p * NT + R * u + c), P.table, lut, P.Q, cc[c]);
-              }
-              float yy = ni[c];
-#pragma unroll
-              for (int v = 0; v < V; ++v) {
-                const float d = fmaf(cc[c][v], sk, nw[v]);
-                yy = fmaf(-d, d, yy);
-              }
-              y[c] = yy;
+              for (int v = 0; v < V; ++v) hh[c][v] = hc[i][p][c][v];
+            } else {
+              raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)c, (uint32_t)(p * NT + R * u + c), P.table,
+                                    lut, P.Q, hh[c]);
             }
-            float M = y[0];
-#pragma unroll
-            for (int c = 1; c < R; ++c) M = fmaxf(M, y[c]);
-            float e[R];
-            float ssum = 0.0f;
-#pragma unroll
-            for (int c = 0; c < R; ++c) {
-              e[c] = fexp2(y[c] - M);
-              ssum += e[c];
-            }
-            const float no = M + flog2(ssum);
-            const float G = fexp2(M + mi[pp] + Kt);
-            if (P.P_out) {  // diagnostics (small B): P, log alpha, log beta in nats
-              const float Ct = (float)cvec[t];
-              const float Dt = (float)(D + (double)Qv);
-              const size_t base = ((size_t)b * N + t) * ((size_t)NT << KV) + (size_t)p * NT + (size_t)R * u;
-#pragma unroll
-              for (int c = 0; c < R; ++c) {
-                P.P_out[base + c] = e[c] * G;
-                P.la_out[base + c] = (y[c] - ni[c] + mi[pp] + Ct) * (float)kLn2;
-                P.lb_out[base + c] = (ni[c] + Dt) * (float)kLn2;
-              }
-            }
+            float yy = nr[c];
 #pragma unroll
             for (int v = 0; v < V; ++v) {
-              float ec = 0.0f;
-#pragma unroll
-              for (int c = 0; c < R; ++c) ec = fmaf(e[c], cc[c][v], ec);
-              acc[v] = fmaf(G, ec, acc[v]);
+              const float d = fmaf(hh[c][v], ssk, nw[v]);
+              yy = fmaf(-d, d, yy);
             }
-            cur[p * NB + u] = no;
-            tmax = fmaxf(tmax, no);
+            y[c] = yy;
+          }
+          float M = 0.0f;
+          if constexpr (SHIFT) {
+            M = y[0];
+#pragma unroll
+            for (int c = 1; c < R; ++c) M = fmaxf(M, y[c]);
+          }
+          float e[R], s = 0.0f, ec[V];
+#pragma unroll
+          for (int c = 0; c < R; ++c) {
+            e[c] = fexp2(y[c] - M);
+            s = c ? s + e[c] : e[c];
+#pragma unroll
+            for (int v = 0; v < V; ++v) ec[v] = c ? fmaf(e[c], hh[c][v], ec[v]) : e[c] * hh[c][v];
+          }
+          const float G = fexp2(pms + M);
+#pragma unroll
+          for (int v = 0; v < V; ++v) cs[v] = G * ec[v];
+          no = flog2(s) + (M - oout);
+          if constexpr (INTERNALS) {  // diagnostics (small B): P, log alpha, log beta in nats
+            const float Ct = (float)cvec[t];
+            const float Dt = (float)D;
+            const size_t base = ((size_t)b * N + t) * ((size_t)NT << KV) + (size_t)p * NT + (size_t)R * u;
+#pragma unroll
+            for (int c = 0; c < R; ++c) {
+              P.P_out[base + c] = e[c] * G;
+              P.la_out[base + c] = (y[c] - nr[c] + pmr + Ct) * (float)kLn2;
+              P.lb_out[base + c] = (n[c] + Dt) * (float)kLn2;
+            }
+          }
+          return s;
+        };
+
+        float acc[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[v] = 0.0f;
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+          const int q = tid + i * nthr;
+          // Consume the head of the pair and fetch the butterfly two ahead:
+          // (t, i+2), or one of an earlier step once this step's run out.
+          float pm[R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            pm[r] = pa[r];
+            pa[r] = pb[r];
+          }
+          if constexpr (kPair) {
+            if (i + 2 < UPT) {
+              load_vec<R>(slot_src(t, i + 2), pb);
+            } else {
+              const int tt = t - 1 - (i + 2 - UPT) / UPT;
+              if (tt >= 0) load_vec<R>(slot_src(tt, (i + 2 - UPT) % UPT), pb);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          if (q < NB) {
+            const int u = CACHE ? q : opaque(q);
+            float n[R];
+            if (t != N - 1) {
+              load_vec<R>(prev + R * u, n);
+            } else {
+#pragma unroll
+              for (int c = 0; c < R; ++c) n[c] = 0.0f;
+            }
+            float Mu = n[0];
+#pragma unroll
+            for (int c = 1; c < R; ++c) Mu = fmaxf(Mu, n[c]);
+            const float sh = -Mu;
+            float nr[R];
+#pragma unroll
+            for (int c = 0; c < R; ++c) nr[c] = n[c] + sh;
+            const uint32_t xu = CT::A * (uint32_t)(R * u) + CT::B;
+            const float oout = sh + Qv;
+            const float kts = Kt - sh;
+            if constexpr (kPair) {
+              float no[R], smin = 0.0f, ua[V];
+#pragma unroll
+              for (int v = 0; v < V; ++v) ua[v] = 0.0f;
+#pragma unroll
+              for (int p = 0; p < R; ++p) {
+                float cs[V];
+                const float s = beta_out(Fast{}, i, p, xu, u, nr, n, pm[p] + kts, pm[p], oout, no[p], cs);
+                smin = p ? fminf(smin, s) : s;
+#pragma unroll
+                for (int v = 0; v < V; ++v) ua[v] += cs[v];
+              }
+              if constexpr (!EXACT) {
+                if (smin < kUnderflow) {
+#pragma unroll
+                  for (int v = 0; v < V; ++v) ua[v] = 0.0f;
+#pragma unroll
+                  for (int p = 0; p < R; ++p) {
+                    float cs[V];
+                    beta_out(std::true_type{}, i, p, xu, u, nr, n, pm[p] + kts, pm[p], oout, no[p], cs);
+#pragma unroll
+                    for (int v = 0; v < V; ++v) ua[v] += cs[v];
+                  }
+                }
+              }
+#pragma unroll
+              for (int v = 0; v < V; ++v) acc[v] += ua[v];
+#pragma unroll
+              for (int p = 0; p < R; ++p) {
+                cur[p * NB + u] = no[p];
+                tmax = fmaxf(tmax, no[p]);
+              }
+            } else {
+              const float* src = slot_src(t, i);
+#pragma unroll 1
+              for (int p = 0; p < R; ++p) {
+                float no, cs[V];
+                const float pmr = src[p];
+                const float s = beta_out(Fast{}, i, p, xu, u, nr, n, pmr + kts, pmr, oout, no, cs);
+                if (!EXACT && s < kUnderflow) beta_out(std::true_type{}, i, p, xu, u, nr, n, pmr + kts, pmr, oout, no, cs);
+#pragma unroll
+                for (int v = 0; v < V; ++v) acc[v] += cs[v];
+                cur[p * NB + u] = no;
+                tmax = fmaxf(tmax, no);
+              }
+            }
           }
         }
-      }
-      D += (double)Qv;
+        D += (double)Qv;
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        const float s = wave_sum(acc[v]);
-        if (lane == 0) spart[(t * nwaves + wave) * V + v] = s;
+        for (int v = 0; v < V; ++v) {
+          const float s = wave_sum(acc[v]);
+          if (lane == 0) spart[(t * nwaves + wave) * V + v] = s * CT::kSigma;
+        }
+        tmax = wave_max(tmax);
+        if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
+        __syncthreads();
       }
-      tmax = wave_max(tmax);
-      if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
-      __syncthreads();
+    };
+    if (Tb < kExactBelowT) {
+      sweeps(std::true_type{});
+    } else {
+      sweeps(std::false_type{});
     }
 
     float* softb = P.soft + (size_t)b * N * V;
@@ -276,9 +427,11 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   }
 }
 
-#define BCJR_FWD_CASE(KV_, V_, CODE_, UPT_, CACHE_)                                        \
-  if (KV == KV_ && V == V_ && code == CODE_ && upt == UPT_ && cache == CACHE_)             \
-    return reinterpret_cast<const void*>(&bcjr_fwd_kernel<KV_, V_, CODE_, UPT_, CACHE_>);
+#define BCJR_FWD_CASE(KV_, V_, CODE_, UPT_, CACHE_)                                          \
+  if (KV == KV_ && V == V_ && code == CODE_ && upt == UPT_ && cache == CACHE_)               \
+    return internals                                                                          \
+        ? reinterpret_cast<const void*>(&bcjr_fwd_kernel<KV_, V_, CODE_, UPT_, CACHE_, true>)  \
+        : reinterpret_cast<const void*>(&bcjr_fwd_kernel<KV_, V_, CODE_, UPT_, CACHE_, false>);
 
 #define BCJR_FWD_UPTS(KV_, V_, CODE_, CACHE_) \
   BCJR_FWD_CASE(KV_, V_, CODE_, 1, CACHE_)    \
@@ -286,13 +439,20 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   BCJR_FWD_CASE(KV_, V_, CODE_, 4, CACHE_)    \
   BCJR_FWD_CASE(KV_, V_, CODE_, 8, CACHE_)
 
-const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool cache) {
+const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool cache, bool internals) {
   // kV = 1: k = 1, V = 1 (table only)
   BCJR_FWD_CASE(1, 1, CODE_TABLE, 1, true)
-  // kV = 2, V = 1: the production scalar codes; cached codewords.
+  // kV = 2, V = 1: the production scalar codes; cached codewords up to 4
+  // butterflies per thread, hashed per state at 8.
   BCJR_FWD_UPTS(2, 1, CODE_TABLE, true)
-  BCJR_FWD_UPTS(2, 1, CODE_1MAD, true)
-  BCJR_FWD_UPTS(2, 1, CODE_3INST, true)
+  BCJR_FWD_CASE(2, 1, CODE_1MAD, 1, true)
+  BCJR_FWD_CASE(2, 1, CODE_1MAD, 2, true)
+  BCJR_FWD_CASE(2, 1, CODE_1MAD, 4, true)
+  BCJR_FWD_CASE(2, 1, CODE_1MAD, 8, false)
+  BCJR_FWD_CASE(2, 1, CODE_3INST, 1, true)
+  BCJR_FWD_CASE(2, 1, CODE_3INST, 2, true)
+  BCJR_FWD_CASE(2, 1, CODE_3INST, 4, true)
+  BCJR_FWD_CASE(2, 1, CODE_3INST, 8, false)
   // kV = 2, V = 2 (k = 1): table / HYB, cached up to 4 units per thread.
   BCJR_FWD_CASE(2, 2, CODE_TABLE, 1, true)
   BCJR_FWD_CASE(2, 2, CODE_TABLE, 2, true)
@@ -300,17 +460,12 @@ const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool cache) {
   BCJR_FWD_CASE(2, 2, CODE_HYB, 1, true)
   BCJR_FWD_CASE(2, 2, CODE_HYB, 2, true)
   BCJR_FWD_CASE(2, 2, CODE_HYB, 4, true)
-  // kV = 4: quarter butterflies per unit, codewords on the fly.
+  // kV = 4: whole 16-state butterflies, at most 256 per sequence (L <= 16).
   BCJR_FWD_CASE(4, 1, CODE_TABLE, 1, false)
-  BCJR_FWD_CASE(4, 1, CODE_TABLE, 2, false)
   BCJR_FWD_CASE(4, 1, CODE_1MAD, 1, false)
-  BCJR_FWD_CASE(4, 1, CODE_1MAD, 2, false)
   BCJR_FWD_CASE(4, 1, CODE_3INST, 1, false)
-  BCJR_FWD_CASE(4, 1, CODE_3INST, 2, false)
   BCJR_FWD_CASE(4, 2, CODE_TABLE, 1, false)
-  BCJR_FWD_CASE(4, 2, CODE_TABLE, 2, false)
   BCJR_FWD_CASE(4, 2, CODE_HYB, 1, false)
-  BCJR_FWD_CASE(4, 2, CODE_HYB, 2, false)
   return nullptr;
 }
 

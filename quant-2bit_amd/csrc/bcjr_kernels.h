@@ -12,7 +12,7 @@ struct FwdParams;
 struct BwdParams;
 struct VitParams;
 
-const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool cache);
+const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool cache, bool internals);
 const void* bwd_kernel_ptr(int KV, int V, int code, int upt);
 const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache);
 const void* decode_kernel_ptr(int KV, int V, int code);
@@ -21,7 +21,7 @@ const void* codebook_kernel_ptr(int code);
 // LDS bytes for one workgroup.
 inline size_t fwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {
   const size_t NT = (size_t)1 << (L - KV);
-  size_t b = 8u * (size_t)N;                       // C_t (double)
+  size_t b = 8u * (size_t)((N + 1) & ~1);          // C_t (double), padded to 16 bytes
   b += 4u * (2 * NT + 3 * 16 + (size_t)N * V + (size_t)N * nwaves * V);
   if (code == 3) b += 4u * ((size_t)2 << Q);
   return b;
@@ -29,7 +29,7 @@ inline size_t fwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, i
 
 inline size_t bwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {
   const size_t NT = (size_t)1 << (L - KV);
-  size_t b = 8u * (size_t)N;
+  size_t b = 8u * (size_t)((N + 1) & ~1);
   b += 4u * (2 * NT + 4 * 16 + 2 * (size_t)N * V + (size_t)N * nwaves * (V + 1));
   if (code == 3) b += 4u * ((size_t)2 << Q);
   return b;

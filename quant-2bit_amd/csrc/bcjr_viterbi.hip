@@ -65,7 +65,7 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
       for (int p = 0; p < R; ++p)
 #pragma unroll
         for (int r = 0; r < R; ++r)
-          codeword<CODE, V, true>((uint32_t)(p * NT + R * u + r), P.table, lut, P.Q, cw[i][p][r]);
+          codeword<CODE, V>((uint32_t)(p * NT + R * u + r), P.table, lut, P.Q, cw[i][p][r]);
     }
   }
 
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
 #pragma unroll
                 for (int v = 0; v < V; ++v) c[v] = cw[i][p][r][v];
               } else {
-                codeword<CODE, V, true>((uint32_t)(p * NT + R * u + rr), P.table, lut, P.Q, c);
+                codeword<CODE, V>((uint32_t)(p * NT + R * u + rr), P.table, lut, P.Q, c);
               }
               float e = 0.0f;
 #pragma unroll
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
       {
         for (int s = tid; s < (NT << KV); s += nthr) {
           float c[V];
-          codeword<CODE, V, true>((uint32_t)s, P.table, lut, P.Q, c);
+          codeword<CODE, V>((uint32_t)s, P.table, lut, P.Q, c);
           float e = 0.0f;
 #pragma unroll
           for (int v = 0; v < V; ++v) {
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
       if (P.walk) P.walk[(size_t)b * N + t] = st;
       if (P.bits) P.bits[(size_t)b * N + t] = st & (R - 1);
       float c[V];
-      codeword<CODE, V, true>((uint32_t)st, P.table, lut, P.Q, c);
+      codeword<CODE, V>((uint32_t)st, P.table, lut, P.Q, c);
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         if (P.recon) P.recon[((size_t)b * N + t) * V + v] = c[v];
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(256) void bcjr_decode_kernel(DecParams P) {
     if (P.walk) P.walk[(size_t)b * P.N + t] = (int32_t)s;
     if (P.recon) {
       float c[V];
-      codeword<CODE, V, true>(s, P.table, P.table, P.Q, c);
+      codeword<CODE, V>(s, P.table, P.table, P.Q, c);
 #pragma unroll
       for (int v = 0; v < V; ++v) P.recon[((size_t)b * P.N + t) * V + v] = c[v];
     }
@@ -295,12 +295,12 @@ __global__ __launch_bounds__(256) void bcjr_codebook_kernel(CbParams P) {
   if (s >= P.S) return;
   if constexpr (CODE == CODE_HYB) {
     float c[2];
-    codeword<CODE_HYB, 2, true>((uint32_t)s, nullptr, P.lut, P.Q, c);
+    codeword<CODE_HYB, 2>((uint32_t)s, nullptr, P.lut, P.Q, c);
     P.out[2 * s] = c[0];
     P.out[2 * s + 1] = c[1];
   } else {
     float c[1];
-    codeword<CODE, 1, true>((uint32_t)s, nullptr, nullptr, P.Q, c);
+    codeword<CODE, 1>((uint32_t)s, nullptr, nullptr, P.Q, c);
     P.out[s] = c[0];
   }
 }
