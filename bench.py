@@ -7,11 +7,19 @@ tiles), 3INST codebook, T=0.1.  One step = forward (soft codewords) + backward
 resident in HBM.  State-updates per step = 4 sweeps (alpha, beta and the two
 adjoint sweeps) x B x N x 2^L cells; recompute sweeps are not counted.
 
-Also reported: per-kernel durations from HIP events on the launch stream, the
-roofline of the dominant kernel against the measured v_exp_f32 issue rate, and
-the CPU oracle (C/OpenMP) timed on a bounded sample of the same workload.
+Also reported:
+  * per-kernel durations from HIP events on the launch stream;
+  * the roofline of the step (both launches) against the measured v_exp_f32
+    issue rate, counting 5 + 2 * 2^-kV algorithmic transcendentals per cell
+    (3 + 2 * 2^-kV of them belong to the soft forward, the other 2 to the
+    gradient);
+  * HBM bytes per step from the committed counter summary
+    (profiles/bcjr_tile_hbm_traffic.txt), when present;
+  * seconds per Llama-3.2-1B decoder-layer QAT step (237,568 sequences), from a
+    4,096-sequence batch timed at each per-tensor temperature of that layer;
+  * the CPU oracle (C/OpenMP) timed on a bounded sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config tile|cpu|layer]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config tile|cpu]
 """
 import argparse
 import ctypes
@@ -24,6 +32,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "quant-2bit_amd"))
 sys.path.insert(0, ROOT)
 
+
 # Algorithmic transcendentals per cell (exp2/log2), structure-aware count:
 #   soft pass: alpha-LSE exp + beta-LSE exp + marginal exp + one log per 2^kV group per sweep
 #   fwd+grad : the soft pass plus one exp per cell for each adjoint sweep
@@ -35,7 +44,13 @@ def trans_per_cell_grad(kV):
     return 5.0 + 2.0 * 2.0 ** (-kV)
 
 
-LAYER_SEQS = 237_568  # Llama-3.2-1B decoder layer: q,o 2048^2; k,v 512x2048; MLP 3x8192x2048
+# Llama-3.2-1B decoder layer: (rows, cols, T) per weight tensor, 256-weight tiles.
+LAYER_TENSORS = (("q", 2048, 2048, 0.05), ("k", 512, 2048, 0.08), ("v", 512, 2048, 0.12),
+                 ("o", 2048, 2048, 0.2), ("gate", 8192, 2048, 0.3), ("up", 8192, 2048, 0.4),
+                 ("down", 2048, 8192, 0.5))
+LAYER_SEQS = sum(r * c // 256 for _, r, c, _ in LAYER_TENSORS)  # 237,568
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "bcjr_tile_hbm_traffic.txt")
+CALIB_BYTES = 256 << 20
 
 
 def parse():
@@ -43,10 +58,11 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="tile", choices=["tile", "cpu", "layer"])
+    ap.add_argument("--config", default="tile", choices=["tile", "cpu"])
     ap.add_argument("--T", type=float, default=0.1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=24, help="sequences in the CPU baseline sample")
+    ap.add_argument("--cpu-sample", type=int, default=256, help="sequences in the CPU baseline sample")
+    ap.add_argument("--no-layer", action="store_true", help="skip the per-temperature layer estimate")
     return ap.parse_args()
 
 
@@ -125,12 +141,9 @@ def main():
     if args.config == "tile":
         L, k, V, N, B, kind = 16, 2, 1, 256, 4096, "3inst"
         workload = "single-tile: L=16 k=2 V=1 N=256 B=4096 (1024x1024 matrix), 3INST, T=%g" % args.T
-    elif args.config == "cpu":
+    else:
         L, k, V, N, B, kind = 12, 2, 1, 256, 128, "1mad"
         workload = "cpu-config: L=12 k=2 V=1 N=256 B=128, 1MAD, T=%g" % args.T
-    else:
-        L, k, V, N, B, kind = 16, 2, 1, 256, LAYER_SEQS, "3inst"
-        workload = "llama-3.2-1b layer: L=16 k=2 V=1 N=256 B=237568, 3INST, T=%g" % args.T
     kV = k * V
     rng = np.random.default_rng(0)
     seq_np = rng.standard_normal((B, N, V)).astype(np.float32)
@@ -177,21 +190,31 @@ def main():
 
     peaks = measure_peaks(torch, dev)
     exp_peak = peaks["exp"]["per_s"]
-    dominant = "bcjr_bwd_kernel" if bwd_s >= fwd_s else "bcjr_fwd_kernel"
-    per_cell = trans_per_cell_grad(kV) if dominant == "bcjr_bwd_kernel" else trans_per_cell_soft(kV)
-    dur = bwd_s if dominant == "bcjr_bwd_kernel" else fwd_s
-    achieved = per_cell * cells / dur
+    # Roofline of one QAT step (forward + backward launches).
+    step_s = fwd_s + bwd_s
+    per_cell = trans_per_cell_grad(kV)
+    achieved = per_cell * cells / step_s
+    traffic = read_traffic()
     roofline = {
-        "bound": "valu_exp", "kernel": dominant,
+        "bound": "valu_exp", "kernel": "bcjr_fwd_kernel+bcjr_bwd_kernel",
         "achieved": achieved / 1e12, "peak": exp_peak / 1e12, "unit": "Texp/s",
-        "frac": achieved / exp_peak, "traffic": None,
-        "per_cell": per_cell, "cells": cells, "launch_s": dur,
+        "frac": achieved / exp_peak, "traffic": traffic,
+        "per_cell": per_cell, "cells": cells, "launch_s": step_s,
     }
+    if traffic is not None:
+        roofline["hbm_GB_s"] = traffic / step_s / 1e9
+        roofline["hbm_frac"] = traffic / step_s / 8e12
+    soft_pc, grad_pc = trans_per_cell_soft(kV), trans_per_cell_grad(kV) - trans_per_cell_soft(kV)
     kernels = {
-        "bcjr_fwd_kernel": {"ms": fwd_s * 1e3, "algorithmic_Texp_s": trans_per_cell_soft(kV) * cells / fwd_s / 1e12},
-        "bcjr_bwd_kernel": {"ms": bwd_s * 1e3, "algorithmic_Texp_s": trans_per_cell_grad(kV) * cells / bwd_s / 1e12},
+        "bcjr_fwd_kernel": {"ms": fwd_s * 1e3, "trans_per_cell": soft_pc,
+                            "frac": soft_pc * cells / fwd_s / exp_peak},
+        "bcjr_bwd_kernel": {"ms": bwd_s * 1e3, "trans_per_cell": grad_pc,
+                            "frac": grad_pc * cells / bwd_s / exp_peak},
     }
-    layer_cells = float(LAYER_SEQS) * 256 * 65536
+    layer = None
+    if args.config == "tile" and not args.no_layer:
+        layer = layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev)
+    calibration_copy(torch, dev)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(seq_np, g_np, cb.cpu().numpy(), args.T, L, kV, min(args.cpu_sample, B))
@@ -202,12 +225,62 @@ def main():
         "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic N(0,1) sequences (seed 0), upstream gradient N(0,1) (seed 1)",
         "config": {"workload": workload, "L": L, "k": k, "V": V, "N": N, "B": B, "code": kind, "T": args.T},
-        "layer_step_s_est": 4.0 * layer_cells / value,
+        "layer_step_s": layer["seconds"] if layer else None,
+        "layer": layer,
         "roofline": roofline, "kernels": kernels,
         "peaks_per_s": {k_: v["per_s"] for k_, v in peaks.items()},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def read_traffic():
+    """HBM bytes per step (forward + backward launch) from the committed counter
+    summary: the line 'traffic_bytes_per_step: <float>'."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_step:"):
+                return float(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev):
+    """Seconds per Llama-3.2-1B decoder-layer QAT step: one forward + backward
+    over a B-sequence batch timed at each tensor's temperature, scaled by that
+    tensor's sequence count (the work per sequence does not depend on B)."""
+    spec, _ = bcjr.forward_backward._spec_for(cb, L, k, V)
+    x = torch.randn(B, N, V, device=dev, generator=torch.Generator(dev).manual_seed(2))
+    g = torch.randn(B, N, V, device=dev, generator=torch.Generator(dev).manual_seed(3))
+    stream = torch.cuda.current_stream(dev)
+    total, per = 0.0, {}
+    for name, rows, cols, T in LAYER_TENSORS:
+        ops.forward(spec, x, T, None)
+        ops.backward(spec, x, T, None, g)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        ops.forward(spec, x, T, None)
+        ops.backward(spec, x, T, None, g)
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        sec = e0.elapsed_time(e1) / 1e3 * (rows * cols // 256) / B
+        per[name] = {"T": T, "sequences": rows * cols // 256, "seconds": sec}
+        total += sec
+    cells = float(LAYER_SEQS) * N * (1 << L)
+    return {"seconds": total, "sequences": LAYER_SEQS, "tensors": per,
+            "state_updates_per_s": 4.0 * cells / total,
+            "note": "fwd+bwd per tensor timed on a %d-sequence batch at that tensor's T, scaled by its "
+                    "sequence count" % B}
+
+
+def calibration_copy(torch, dev):
+    """One device-to-device copy of CALIB_BYTES: its FETCH_SIZE / WRITE_SIZE
+    counters scale the BCJR kernels' counters to bytes."""
+    src = torch.ones(CALIB_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize(dev)
 
 
 if __name__ == "__main__":
