@@ -25,8 +25,8 @@
 // butterfly's R pairs, computes, and writes its R outputs to the same pairs, with
 // one barrier per step and the next butterfly's pairs read ahead of the current
 // one's arithmetic.  The alpha sweep writes each butterfly's raw inputs (m~ and
-// mu, 2R floats) to the scratch slot; the beta sweep reads them back two
-// butterflies ahead to form P and phi.
+// mu, 2R floats) to the scratch slot; the beta sweep reads them back one step
+// ahead to form P and phi.
 //
 // Group sums take the zero-shift form; a butterfly with any
 // underflowed group (sum < kUnderflow) is recomputed against the group maxima
@@ -103,6 +103,9 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
       wbuf[i] = seqb[i];
       gbuf[i] = gb[i];
     }
+    // (m~_{-1}, mu_{-1}) = (log2(R), 0) for every state: what step 0 reads.
+    for (int j = tid; j < NT; j += nthr) mm[j] = make_float2((float)KV, 0.0f);
+    if (tid < 2 * kMaxWaves) wmax[tid] = -INFINITY;  // waves that do not exist
     __syncthreads();
 
     // Below kExactBelowT most groups would underflow the zero-shift sums, so
@@ -120,7 +123,7 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
         float O = (float)KV;
         if (t > 0) {
           O = -INFINITY;
-          for (int w = 0; w < nwaves; ++w) O = fmaxf(O, wmax[((k + 1) & 1) * kMaxWaves + w]);
+          O = block_max(wmax + ((k + 1) & 1) * kMaxWaves);
         }
         if (tid == 0) cvec[t] = C;
         C += (double)O;
@@ -191,14 +194,9 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
           const uint32_t yi = yb ^ Ku[i];
 #pragma unroll
           for (int p = 0; p < R; ++p) {
-            if (t) {
-              const float2 v2 = lds_pair(yi ^ koff(p));
-              m[p] = v2.x;
-              mu[p] = v2.y;
-            } else {
-              m[p] = (float)KV;
-              mu[p] = 0.0f;
-            }
+            const float2 v2 = lds_pair(yi ^ koff(p));
+            m[p] = v2.x;
+            mu[p] = v2.y;
           }
         };
         // Inputs of the next butterfly are read before the current one's
@@ -273,7 +271,7 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
       // log2 Z and E[F] = sum_j 2^(m_{N-1}(j) - log2 Z) mu_{N-1}(j); m~ and mu of a
       // state share a pair, so the sums run over pairs.
       float Mz = -INFINITY;
-      for (int w = 0; w < nwaves; ++w) Mz = fmaxf(Mz, wmax[((k + 1) & 1) * kMaxWaves + w]);
+      Mz = block_max(wmax + ((k + 1) & 1) * kMaxWaves);
       float ps = 0.0f, pe = 0.0f;
       for (int j = tid; j < NT; j += nthr) {
         const float2 v2 = mm[j];
@@ -295,23 +293,27 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
       }
       const double logZ2 = C + (double)Mz + (double)flog2(Ssum);
       const float EFg = Esum / Ssum - gZ;  // E[F] - g_Z
+      // (n~_{N-1}, nu_{N-1}) = (0, 0): what step N-1 of the beta sweep reads.
+      for (int j = tid; j < NT; j += nthr) mm[j] = make_float2(0.0f, 0.0f);
+      __syncthreads();
 
       // -------------------------- beta + nu + grad sweep -----------------------
-      // Raw alpha-side inputs (m~, mu) of step t come back from HBM two
-      // butterflies ahead of their use, across step boundaries.
+      // Raw alpha-side inputs (m~, mu) of step t come back from HBM one step
+      // ahead of their use.
       auto slot_src = [&](int t, int i) {
         const int q = min(tid + i * nthr, NB - 1);
         return slot + ((size_t)t * NB + q) * 2 * R;
       };
-      float pa[R], pua[R], pb[R], pub[R];  // the next two butterflies in consumption order
-      if (kPair) {
-        load_vec<R>(slot_src(N - 1, 0), pa);
-        load_vec<R>(slot_src(N - 1, 0) + R, pua);
-      }
-      if (kPair && (UPT > 1 || N > 1)) {
-        const float* src = UPT > 1 ? slot_src(N - 1, 1) : slot_src(N - 2, 0);
-        load_vec<R>(src, pb);
-        load_vec<R>(src + R, pub);
+      // Slot inputs of each of this thread's butterflies one step ahead: the
+      // registers of butterfly i are refilled with step t-1 as soon as step t
+      // has consumed them.
+      float pf[kPair ? UPT : 1][R], pfu[kPair ? UPT : 1][R];
+      if constexpr (kPair) {
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+          load_vec<R>(slot_src(N - 1, i), pf[i]);
+          load_vec<R>(slot_src(N - 1, i) + R, pfu[i]);
+        }
       }
       double D = 0.0;  // D_t
       // rho_t = kV * (t - 1) mod nb at t = N - 1
@@ -320,7 +322,7 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
         float Qv = 0.0f;
         if (t != N - 1) {
           Qv = -INFINITY;
-          for (int w = 0; w < nwaves; ++w) Qv = fmaxf(Qv, wmax[((k + 1) & 1) * kMaxWaves + w]);
+          Qv = block_max(wmax + ((k + 1) & 1) * kMaxWaves);
         }
         const float Kt = (float)(cvec[t] + D - logZ2);
         float nw[V], sg[V];
@@ -402,14 +404,9 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
           const uint32_t yi = yb ^ Ku[i];
 #pragma unroll
           for (int c = 0; c < R; ++c) {
-            if (t != N - 1) {
-              const float2 v2 = lds_pair(yi ^ koff(c));
-              n[c] = v2.x;
-              nu[c] = v2.y;
-            } else {
-              n[c] = 0.0f;
-              nu[c] = 0.0f;
-            }
+            const float2 v2 = lds_pair(yi ^ koff(c));
+            n[c] = v2.x;
+            nu[c] = v2.y;
           }
         };
         float nx[R], nxu[R];
@@ -421,24 +418,20 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
           const int q = tid + i * nthr;
-          // Consume the head of the slot pair and fetch the butterfly two ahead.
           float pm[R], pmu[R], ni[R], nui[R];
 #pragma unroll
           for (int r = 0; r < R; ++r) {
-            pm[r] = pa[r];
-            pmu[r] = pua[r];
-            pa[r] = pb[r];
-            pua[r] = pub[r];
+            if constexpr (kPair) {
+              pm[r] = pf[i][r];
+              pmu[r] = pfu[i][r];
+            }
             ni[r] = nx[r];
             nui[r] = nxu[r];
           }
           if constexpr (kPair) {
-            const int tt = i + 2 < UPT ? t : t - 1 - (i + 2 - UPT) / UPT;
-            const int ii = i + 2 < UPT ? i + 2 : (i + 2 - UPT) % UPT;
-            if (tt >= 0) {
-              const float* src = slot_src(tt, ii);
-              load_vec<R>(src, pb);
-              load_vec<R>(src + R, pub);
+            if (t > 0) {
+              load_vec<R>(slot_src(t - 1, i), pf[i]);
+              load_vec<R>(slot_src(t - 1, i) + R, pfu[i]);
             }
           }
           if (i + 1 < UPT) read_in(i + 1, nx, nxu);

@@ -219,6 +219,18 @@ __device__ __forceinline__ uint32_t opaque_uniform(uint32_t x) {
   return x;
 }
 
+// Maximum over the kMaxWaves per-wave entries at w (16-byte aligned; entries of
+// waves that do not exist hold -inf): four broadcast 16-byte LDS reads, no
+// dependent round trips.
+__device__ __forceinline__ float block_max(const float* w) {
+  static_assert(kMaxWaves == 16, "block_max reads four float4");
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  const float4 a = w4[0], b = w4[1], c = w4[2], d = w4[3];
+  const float ab = fmaxf(fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w)), fmaxf(fmaxf(b.x, b.y), fmaxf(b.z, b.w)));
+  const float cd = fmaxf(fmaxf(fmaxf(c.x, c.y), fmaxf(c.z, c.w)), fmaxf(fmaxf(d.x, d.y), fmaxf(d.z, d.w)));
+  return fmaxf(ab, cd);
+}
+
 // ---------------------------------------------------------------------------
 // Wave (64-lane) reductions.  Blocks are always a whole number of waves;
 // threads without work contribute the neutral element.

@@ -89,6 +89,9 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
     const float ssk = CT::kSigma * sk;  // d = (c - w) * sk = h * ssk - w * sk
     const float* seqb = P.seq + (size_t)b * N * V;
     for (int i = tid; i < N * V; i += nthr) wbuf[i] = seqb[i];
+    // m~_{-1} = log2(R) everywhere: the buffer step 0 reads from.
+    for (int j = tid; j < NT; j += nthr) mbuf[NT + j] = (float)KV;
+    if (tid < 2 * kMaxWaves) wmax[tid] = -INFINITY;  // waves that do not exist
     __syncthreads();
 
     double logZ2 = 0.0;
@@ -108,7 +111,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
         float O = (float)KV;  // m~_{-1} = log2(R) for every j
         if (t > 0) {
           O = -INFINITY;
-          for (int w = 0; w < nwaves; ++w) O = fmaxf(O, wmax[((k + 1) & 1) * kMaxWaves + w]);
+          O = block_max(wmax + ((k + 1) & 1) * kMaxWaves);
         }
         if (tid == 0) cvec[t] = C;
         C += (double)O;
@@ -160,16 +163,26 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
           return s;
         };
 
+        // Inputs of butterfly tid + i*nthr; the next butterfly's are read
+        // before the current one's arithmetic (prev is read-only this step).
+        auto read_in = [&](int i, float (&m)[R]) {
+          const int qq = min(tid + i * nthr, NB - 1);
+#pragma unroll
+          for (int p = 0; p < R; ++p) m[p] = prev[p * NB + qq];
+        };
+        float nx[R];
+        read_in(0, nx);
         float tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
           const int q = tid + i * nthr;
+          float m[R];
+#pragma unroll
+          for (int p = 0; p < R; ++p) m[p] = nx[p];
+          if (i + 1 < UPT) read_in(i + 1, nx);
           __builtin_amdgcn_sched_barrier(0);
           if (q < NB) {
             const int u = CACHE ? q : opaque(q);
-            float m[R];
-#pragma unroll
-            for (int p = 0; p < R; ++p) m[p] = t ? prev[p * NB + u] : (float)KV;
             store_vec<R>(slot + ((size_t)t * NB + u) * R, m);
             float Mu = m[0];
 #pragma unroll
@@ -215,7 +228,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
       // log2 Z = C_{N-1} + LSE2 over the final reduced state.
       const float* fin = mbuf + ((k + 1) & 1) * NT;
       float Mz = -INFINITY;
-      for (int w = 0; w < nwaves; ++w) Mz = fmaxf(Mz, wmax[((k + 1) & 1) * kMaxWaves + w]);
+      Mz = block_max(wmax + ((k + 1) & 1) * kMaxWaves);
       float part = 0.0f;
       for (int j = tid; j < NT; j += nthr) part += fexp2(fin[j] - Mz);
       part = wave_sum(part);
@@ -224,17 +237,25 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
       float Ssum = 0.0f;
       for (int w = 0; w < nwaves; ++w) Ssum += wsum[w];
       logZ2 = C + (double)Mz + (double)flog2(Ssum);
+      // n~_{N-1} = 0: the buffer step N-1 of the beta sweep reads from.
+      for (int j = tid; j < NT; j += nthr) mbuf[((k + 1) & 1) * NT + j] = 0.0f;
+      __syncthreads();
 
       // ------------------------------ beta sweep -------------------------------
-      // Raw alpha inputs of step t come back from HBM two butterflies ahead of
-      // their use, across step boundaries.
+      // Raw alpha inputs of step t come back from HBM one step ahead of their
+      // use.
       auto slot_src = [&](int t, int i) {
         const int q = min(tid + i * nthr, NB - 1);
         return slot + ((size_t)t * NB + q) * R;
       };
-      float pa[R], pb[R];  // the next two butterflies in consumption order (t descending, i ascending)
-      if (kPair) load_vec<R>(slot_src(N - 1, 0), pa);
-      if (kPair && (UPT > 1 || N > 1)) load_vec<R>(UPT > 1 ? slot_src(N - 1, 1) : slot_src(N - 2, 0), pb);
+      // Slot inputs of each of this thread's butterflies one step ahead: the
+      // register set of butterfly i is refilled with step t-1 as soon as
+      // step t has consumed it.
+      float pf[kPair ? UPT : 1][R];
+      if constexpr (kPair) {
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) load_vec<R>(slot_src(N - 1, i), pf[i]);
+      }
       double D = 0.0;  // D_t
       for (int t = N - 1; t >= 0; --t, ++k) {
         const float* prev = mbuf + ((k + 1) & 1) * NT;
@@ -242,7 +263,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
         float Qv = 0.0f;
         if (t != N - 1) {
           Qv = -INFINITY;
-          for (int w = 0; w < nwaves; ++w) Qv = fmaxf(Qv, wmax[((k + 1) & 1) * kMaxWaves + w]);
+          Qv = block_max(wmax + ((k + 1) & 1) * kMaxWaves);
         }
         const float Kt = (float)(cvec[t] + D - logZ2);
         float nw[V];
@@ -307,6 +328,9 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
           return s;
         };
 
+        auto read_in = [&](int i, float (&n)[R]) { load_vec<R>(prev + R * min(tid + i * nthr, NB - 1), n); };
+        float nx[R];
+        read_in(0, nx);
         float acc[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) acc[v] = 0.0f;
@@ -314,32 +338,19 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
           const int q = tid + i * nthr;
-          // Consume the head of the pair and fetch the butterfly two ahead:
-          // (t, i+2), or one of an earlier step once this step's run out.
-          float pm[R];
+          float pm[R], n[R];
 #pragma unroll
           for (int r = 0; r < R; ++r) {
-            pm[r] = pa[r];
-            pa[r] = pb[r];
+            n[r] = nx[r];
+            if constexpr (kPair) pm[r] = pf[i][r];
           }
           if constexpr (kPair) {
-            if (i + 2 < UPT) {
-              load_vec<R>(slot_src(t, i + 2), pb);
-            } else {
-              const int tt = t - 1 - (i + 2 - UPT) / UPT;
-              if (tt >= 0) load_vec<R>(slot_src(tt, (i + 2 - UPT) % UPT), pb);
-            }
+            if (t > 0) load_vec<R>(slot_src(t - 1, i), pf[i]);
           }
+          if (i + 1 < UPT) read_in(i + 1, nx);
           __builtin_amdgcn_sched_barrier(0);
           if (q < NB) {
             const int u = CACHE ? q : opaque(q);
-            float n[R];
-            if (t != N - 1) {
-              load_vec<R>(prev + R * u, n);
-            } else {
-#pragma unroll
-              for (int c = 0; c < R; ++c) n[c] = 0.0f;
-            }
             float Mu = n[0];
 #pragma unroll
             for (int c = 1; c < R; ++c) Mu = fmaxf(Mu, n[c]);
