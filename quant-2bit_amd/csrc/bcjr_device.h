@@ -235,16 +235,37 @@ __device__ __forceinline__ float block_max(const float* w) {
 // Wave (64-lane) reductions.  Blocks are always a whole number of waves;
 // threads without work contribute the neutral element.
 // ---------------------------------------------------------------------------
+// DPP move of v within rows of 16 lanes (CTRL: quad_perm, row mirrors).
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int kDppSwap1 = 0xB1;       // quad_perm [1, 0, 3, 2]
+constexpr int kDppSwap2 = 0x4E;       // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror
+constexpr int kDppMirror = 0x140;     // row_mirror
+
+__device__ __forceinline__ float lane_of(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// Wave results are uniform: four DPP steps leave each row's reduction in every
+// lane of the row, and four readlanes combine the rows.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_row<kDppSwap1>(v));
+  v = fmaxf(v, dpp_row<kDppSwap2>(v));
+  v = fmaxf(v, dpp_row<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_row<kDppMirror>(v));
+  return fmaxf(fmaxf(lane_of(v, 0), lane_of(v, 16)), fmaxf(lane_of(v, 32), lane_of(v, 48)));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_row<kDppSwap1>(v);
+  v += dpp_row<kDppSwap2>(v);
+  v += dpp_row<kDppHalfMirror>(v);
+  v += dpp_row<kDppMirror>(v);
+  return (lane_of(v, 0) + lane_of(v, 16)) + (lane_of(v, 32) + lane_of(v, 48));
 }
 
 // ---------------------------------------------------------------------------
