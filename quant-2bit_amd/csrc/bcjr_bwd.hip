@@ -214,7 +214,6 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
             mui[p] = nxu[p];
           }
           if (i + 1 < UPT) read_in(i + 1, nx, nxu);
-          __builtin_amdgcn_sched_barrier(0);
           if (q < NB) {
             const int u = opaque(q);
             {
@@ -435,7 +434,6 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
             }
           }
           if (i + 1 < UPT) read_in(i + 1, nx, nxu);
-          __builtin_amdgcn_sched_barrier(0);
           if (q < NB) {
             const int u = opaque(q);
             float Mu = ni[0];

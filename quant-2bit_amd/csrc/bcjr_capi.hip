@@ -255,14 +255,11 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
   const int N = (int)p->N;
   if (op == OP_FWD || op == OP_FWD_INTERNALS || op == OP_VIT) {
     const bool fwd = (op != OP_VIT);
-    // Codeword cache in VGPRs: up to 128 per thread for tables and the
-    // Viterbi kernel; the soft forward keeps hash codes in registers only up to
-    // 64 (at 8 butterflies per thread the cache would spill, and a hash costs
-    // three VALU per state).
-    const bool hash = p->code == BCJR_CODE_1MAD || p->code == BCJR_CODE_3INST;
-    const int cache_max = (fwd && hash) ? 64 : 128;
-    pl->cache = (pl->NSUB == 1) && (upt * R * R * p->V <= cache_max);
-    pl->fn = fwd ? bcjr::fwd_kernel_ptr(KV, p->V, p->code, upt, pl->cache, op == OP_FWD_INTERNALS)
+    // The Viterbi kernel caches all of a thread's codewords in VGPRs up to 128
+    // of them; the soft forward's cache is fixed per instance
+    // (fwd_cached_units).
+    pl->cache = !fwd && (pl->NSUB == 1) && (upt * R * R * p->V <= 128);
+    pl->fn = fwd ? bcjr::fwd_kernel_ptr(KV, p->V, p->code, upt, op == OP_FWD_INTERNALS)
                  : bcjr::vit_kernel_ptr(KV, p->V, p->code, upt, pl->cache);
     pl->lds = fwd ? bcjr::fwd_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q)
                   : bcjr::vit_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q);

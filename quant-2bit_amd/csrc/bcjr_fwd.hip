@@ -34,13 +34,14 @@
 
 namespace bcjr {
 
-template <int KV, int V, int CODE, int UPT, bool CACHE, bool INTERNALS>
+template <int KV, int V, int CODE, int UPT, int CU, bool INTERNALS>
 __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   constexpr int R = 1 << KV;
   // Butterflies of 2 or 4 states run fully unrolled with their slot inputs
   // prefetched in registers; 16-state butterflies loop over outputs.
   constexpr bool kPair = R <= 4;
-  static_assert(!CACHE || kPair, "codeword cache is for butterflies of at most 4 states");
+  static_assert(CU == 0 || kPair, "codeword cache is for butterflies of at most 4 states");
+  static_assert(CU <= UPT, "at most UPT cached butterflies");
   using CT = CodeTraits<CODE>;
 
   extern __shared__ __align__(16) unsigned char smem[];
@@ -65,11 +66,12 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
     __syncthreads();
   }
 
-  // Raw codewords h of this thread's butterflies, fixed for the whole launch.
-  float hc[CACHE ? UPT : 1][CACHE ? R : 1][CACHE ? R : 1][V];
-  if constexpr (CACHE) {
+  // Raw codewords h of this thread's first CU butterflies, fixed for the
+  // whole launch; the others are hashed per state.
+  float hc[CU > 0 ? CU : 1][CU > 0 ? R : 1][CU > 0 ? R : 1][V];
+  if constexpr (CU > 0) {
 #pragma unroll
-    for (int i = 0; i < UPT; ++i) {
+    for (int i = 0; i < CU; ++i) {
       const int u = min(tid + i * nthr, NB - 1);
       const uint32_t xu = CT::A * (uint32_t)(R * u) + CT::B;
 #pragma unroll
@@ -130,14 +132,15 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
             float acc = m[p];
             // The two-rounding d_3inst form is kept out of the low-temperature
             // variant, where |d| reaches ~1e2 and float32 precision is tightest.
-            if constexpr (!CACHE && CODE == CODE_3INST && !EXACT) {
+            const bool cached = i < CU;
+            if (!cached && CODE == CODE_3INST && !EXACT) {
               const float d = d_3inst(xu + p * ANT + CT::A * (uint32_t)r, ssk, nw[0]);
               acc = fmaf(-d, d, acc);
             } else {
               float h[V];
-              if constexpr (CACHE) {
+              if (cached) {
 #pragma unroll
-                for (int v = 0; v < V; ++v) h[v] = hc[i][p][r][v];
+                for (int v = 0; v < V; ++v) h[v] = hc[cached ? i : 0][p][r][v];
               } else {
                 raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)r, (uint32_t)(p * NT + R * u + r), P.table,
                                       lut, P.Q, h);
@@ -180,9 +183,8 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 #pragma unroll
           for (int p = 0; p < R; ++p) m[p] = nx[p];
           if (i + 1 < UPT) read_in(i + 1, nx);
-          __builtin_amdgcn_sched_barrier(0);
           if (q < NB) {
-            const int u = CACHE ? q : opaque(q);
+            const int u = i < CU ? q : opaque(q);
             store_vec<R>(slot + ((size_t)t * NB + u) * R, m);
             float Mu = m[0];
 #pragma unroll
@@ -281,9 +283,9 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
           float y[R], hh[R][V];
 #pragma unroll
           for (int c = 0; c < R; ++c) {
-            if constexpr (CACHE) {
+            if (i < CU) {
 #pragma unroll
-              for (int v = 0; v < V; ++v) hh[c][v] = hc[i][p][c][v];
+              for (int v = 0; v < V; ++v) hh[c][v] = hc[i < CU ? i : 0][p][c][v];
             } else {
               raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)c, (uint32_t)(p * NT + R * u + c), P.table,
                                     lut, P.Q, hh[c]);
@@ -348,9 +350,8 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
             if (t > 0) load_vec<R>(slot_src(t - 1, i), pf[i]);
           }
           if (i + 1 < UPT) read_in(i + 1, nx);
-          __builtin_amdgcn_sched_barrier(0);
           if (q < NB) {
-            const int u = CACHE ? q : opaque(q);
+            const int u = i < CU ? q : opaque(q);
             float Mu = n[0];
 #pragma unroll
             for (int c = 1; c < R; ++c) Mu = fmaxf(Mu, n[c]);
@@ -438,45 +439,32 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   }
 }
 
-#define BCJR_FWD_CASE(KV_, V_, CODE_, UPT_, CACHE_)                                          \
-  if (KV == KV_ && V == V_ && code == CODE_ && upt == UPT_ && cache == CACHE_)               \
-    return internals                                                                          \
-        ? reinterpret_cast<const void*>(&bcjr_fwd_kernel<KV_, V_, CODE_, UPT_, CACHE_, true>)  \
-        : reinterpret_cast<const void*>(&bcjr_fwd_kernel<KV_, V_, CODE_, UPT_, CACHE_, false>);
+#define BCJR_FWD_CASE(KV_, V_, CODE_, UPT_)                                                      \
+  if (KV == KV_ && V == V_ && code == CODE_ && upt == UPT_) {                                   \
+    constexpr int CU_ = fwd_cached_units(KV_, V_, UPT_);                                        \
+    return internals ? reinterpret_cast<const void*>(&bcjr_fwd_kernel<KV_, V_, CODE_, UPT_, CU_, true>) \
+                     : reinterpret_cast<const void*>(&bcjr_fwd_kernel<KV_, V_, CODE_, UPT_, CU_, false>); \
+  }
 
-#define BCJR_FWD_UPTS(KV_, V_, CODE_, CACHE_) \
-  BCJR_FWD_CASE(KV_, V_, CODE_, 1, CACHE_)    \
-  BCJR_FWD_CASE(KV_, V_, CODE_, 2, CACHE_)    \
-  BCJR_FWD_CASE(KV_, V_, CODE_, 4, CACHE_)    \
-  BCJR_FWD_CASE(KV_, V_, CODE_, 8, CACHE_)
+#define BCJR_FWD_UPTS(KV_, V_, CODE_) \
+  BCJR_FWD_CASE(KV_, V_, CODE_, 1)    \
+  BCJR_FWD_CASE(KV_, V_, CODE_, 2)    \
+  BCJR_FWD_CASE(KV_, V_, CODE_, 4)    \
+  BCJR_FWD_CASE(KV_, V_, CODE_, 8)
 
-const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool cache, bool internals) {
-  // kV = 1: k = 1, V = 1 (table only)
-  BCJR_FWD_CASE(1, 1, CODE_TABLE, 1, true)
-  // kV = 2, V = 1: the production scalar codes; cached codewords up to 4
-  // butterflies per thread, hashed per state at 8.
-  BCJR_FWD_UPTS(2, 1, CODE_TABLE, true)
-  BCJR_FWD_CASE(2, 1, CODE_1MAD, 1, true)
-  BCJR_FWD_CASE(2, 1, CODE_1MAD, 2, true)
-  BCJR_FWD_CASE(2, 1, CODE_1MAD, 4, true)
-  BCJR_FWD_CASE(2, 1, CODE_1MAD, 8, false)
-  BCJR_FWD_CASE(2, 1, CODE_3INST, 1, true)
-  BCJR_FWD_CASE(2, 1, CODE_3INST, 2, true)
-  BCJR_FWD_CASE(2, 1, CODE_3INST, 4, true)
-  BCJR_FWD_CASE(2, 1, CODE_3INST, 8, false)
-  // kV = 2, V = 2 (k = 1): table / HYB, cached up to 4 units per thread.
-  BCJR_FWD_CASE(2, 2, CODE_TABLE, 1, true)
-  BCJR_FWD_CASE(2, 2, CODE_TABLE, 2, true)
-  BCJR_FWD_CASE(2, 2, CODE_TABLE, 4, true)
-  BCJR_FWD_CASE(2, 2, CODE_HYB, 1, true)
-  BCJR_FWD_CASE(2, 2, CODE_HYB, 2, true)
-  BCJR_FWD_CASE(2, 2, CODE_HYB, 4, true)
+const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool internals) {
+  BCJR_FWD_CASE(1, 1, CODE_TABLE, 1)  // kV = 1: k = 1, V = 1 (L <= 11)
+  BCJR_FWD_UPTS(2, 1, CODE_TABLE)
+  BCJR_FWD_UPTS(2, 1, CODE_1MAD)
+  BCJR_FWD_UPTS(2, 1, CODE_3INST)
+  BCJR_FWD_UPTS(2, 2, CODE_TABLE)
+  BCJR_FWD_UPTS(2, 2, CODE_HYB)
   // kV = 4: whole 16-state butterflies, at most 256 per sequence (L <= 16).
-  BCJR_FWD_CASE(4, 1, CODE_TABLE, 1, false)
-  BCJR_FWD_CASE(4, 1, CODE_1MAD, 1, false)
-  BCJR_FWD_CASE(4, 1, CODE_3INST, 1, false)
-  BCJR_FWD_CASE(4, 2, CODE_TABLE, 1, false)
-  BCJR_FWD_CASE(4, 2, CODE_HYB, 1, false)
+  BCJR_FWD_CASE(4, 1, CODE_TABLE, 1)
+  BCJR_FWD_CASE(4, 1, CODE_1MAD, 1)
+  BCJR_FWD_CASE(4, 1, CODE_3INST, 1)
+  BCJR_FWD_CASE(4, 2, CODE_TABLE, 1)
+  BCJR_FWD_CASE(4, 2, CODE_HYB, 1)
   return nullptr;
 }
 

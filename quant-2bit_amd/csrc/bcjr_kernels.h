@@ -12,7 +12,17 @@ struct FwdParams;
 struct BwdParams;
 struct VitParams;
 
-const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool cache, bool internals);
+// Butterflies per thread (of upt) whose codewords the soft forward keeps in
+// VGPRs for the whole launch: as many as fit kFwdCacheVgprs (R*R*V each);
+// 16-state butterflies are never cached.
+constexpr int kFwdCacheVgprs = 64;
+constexpr int fwd_cached_units(int KV, int V, int upt) {
+  return KV >= 4 ? 0
+                 : (upt < kFwdCacheVgprs / ((1 << KV) * (1 << KV) * V) ? upt
+                                                                        : kFwdCacheVgprs / ((1 << KV) * (1 << KV) * V));
+}
+
+const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool internals);
 const void* bwd_kernel_ptr(int KV, int V, int code, int upt);
 const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache);
 const void* decode_kernel_ptr(int KV, int V, int code);
