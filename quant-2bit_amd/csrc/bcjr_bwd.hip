@@ -25,8 +25,9 @@
 // butterfly's R pairs, computes, and writes its R outputs to the same pairs, with
 // one barrier per step and the next butterfly's pairs read ahead of the current
 // one's arithmetic.  The alpha sweep writes each butterfly's raw inputs (m~ and
-// mu, 2R floats) to the scratch slot; the beta sweep reads them back one step
-// ahead to form P and phi.
+// mu, 2R floats) to the scratch slot; the beta sweep reads them back two
+// butterflies ahead to form P and phi.  The codewords of a thread's first few
+// butterflies stay in VGPRs for the launch (bwd_cached_units).
 //
 // Group sums take the zero-shift form; a butterfly with any
 // underflowed group (sum < kUnderflow) is recomputed against the group maxima
@@ -40,7 +41,7 @@ namespace bcjr {
 template <int R>
 constexpr int kOuterUnroll = R <= 4 ? R : 1;
 
-template <int KV, int V, int CODE, int UPT>
+template <int KV, int V, int CODE, int UPT, int CU>
 __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
   constexpr int R = 1 << KV;
   using CT = CodeTraits<CODE>;
@@ -48,6 +49,8 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
   // inputs prefetched in registers; 16-state butterflies loop over outputs and
   // read those inputs from the slot as they go.
   constexpr bool kPair = R <= 4;
+  static_assert(CU == 0 || kPair, "codeword cache is for butterflies of at most 4 states");
+  static_assert(CU <= UPT, "at most UPT cached butterflies");
 
   extern __shared__ __align__(16) unsigned char smem[];
   const int L = P.L, N = P.N;
@@ -74,6 +77,24 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
     const int nl = 2 << P.Q;
     for (int i = tid; i < nl; i += nthr) lut[i] = P.table[i];
     __syncthreads();
+  }
+
+  // Raw codewords h of this thread's first CU butterflies (hc[i][p][c] for
+  // state p*NT + R*u + c), fixed for the whole launch; the others are hashed
+  // per state in each sweep.
+  float hc[CU > 0 ? CU : 1][CU > 0 ? R : 1][CU > 0 ? R : 1][V];
+  if constexpr (CU > 0) {
+#pragma unroll
+    for (int i = 0; i < CU; ++i) {
+      const int u = min(tid + i * nthr, NB - 1);
+      const uint32_t xu = CT::A * (uint32_t)(R * u) + CT::B;
+#pragma unroll
+      for (int p = 0; p < R; ++p)
+#pragma unroll
+        for (int c = 0; c < R; ++c)
+          raw_codeword<CODE, V>(xu, CT::A * (uint32_t)(p * NT + c), (uint32_t)(p * NT + R * u + c), P.table, lut,
+                                P.Q, hc[i][p][c]);
+    }
   }
 
   // Byte address of slot k of butterfly tid + i*nthr at rotation rho:
@@ -151,15 +172,20 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
 
         // Output r of butterfly u: m~ and mu of state R*u + r from the shifted
         // inputs m[p] (maximum 0) and the raw mu inputs; returns the group sum.
-        auto alpha_out = [&](auto shift_tag, int r, uint32_t xu, int u, const float (&m)[R],
+        auto alpha_out = [&](auto shift_tag, int i, int r, uint32_t xu, int u, const float (&m)[R],
                              const float (&mui)[R], float oout, float& mo, float& muo) -> float {
           constexpr bool SHIFT = decltype(shift_tag)::value;
           float a[R], phi[R];
 #pragma unroll
           for (int p = 0; p < R; ++p) {
             float h[V];
-            raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)r, (uint32_t)(p * NT + R * u + r), P.table,
-                                  lut, P.Q, h);
+            if (i < CU) {
+#pragma unroll
+              for (int v = 0; v < V; ++v) h[v] = hc[i < CU ? i : 0][p][r][v];
+            } else {
+              raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)r, (uint32_t)(p * NT + R * u + r), P.table,
+                                    lut, P.Q, h);
+            }
             float acc = m[p];
             float ph = mui[p];
 #pragma unroll
@@ -215,7 +241,7 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
           }
           if (i + 1 < UPT) read_in(i + 1, nx, nxu);
           if (q < NB) {
-            const int u = opaque(q);
+            const int u = i < CU ? q : opaque(q);
             {
               float* dst = slot + ((size_t)t * NB + u) * 2 * R;
               store_vec<R>(dst, mi);
@@ -235,13 +261,13 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
               float mo[R], muo[R], smin = 0.0f;
 #pragma unroll
               for (int r = 0; r < R; ++r) {
-                const float s = alpha_out(Fast{}, r, xu, u, m, mui, oout, mo[r], muo[r]);
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, mui, oout, mo[r], muo[r]);
                 smin = r ? fminf(smin, s) : s;
               }
               if constexpr (!EXACT) {
                 if (smin < kUnderflow) {
 #pragma unroll
-                  for (int r = 0; r < R; ++r) alpha_out(std::true_type{}, r, xu, u, m, mui, oout, mo[r], muo[r]);
+                  for (int r = 0; r < R; ++r) alpha_out(std::true_type{}, i, r, xu, u, m, mui, oout, mo[r], muo[r]);
                 }
               }
 #pragma unroll
@@ -253,8 +279,8 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
 #pragma unroll kOuterUnroll<R>
               for (int r = 0; r < R; ++r) {
                 float mo, muo;
-                const float s = alpha_out(Fast{}, r, xu, u, m, mui, oout, mo, muo);
-                if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, r, xu, u, m, mui, oout, mo, muo);
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, mui, oout, mo, muo);
+                if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, i, r, xu, u, m, mui, oout, mo, muo);
                 lds_pair(yi ^ koff(r)) = make_float2(mo, muo);
                 tmax = fmaxf(tmax, mo);
               }
@@ -297,21 +323,22 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
       __syncthreads();
 
       // -------------------------- beta + nu + grad sweep -----------------------
-      // Raw alpha-side inputs (m~, mu) of step t come back from HBM one step
-      // ahead of their use.
+      // Raw alpha-side inputs (m~, mu) of step t come back from HBM two
+      // butterflies ahead of their use, across step boundaries.
       auto slot_src = [&](int t, int i) {
         const int q = min(tid + i * nthr, NB - 1);
         return slot + ((size_t)t * NB + q) * 2 * R;
       };
-      // Slot inputs of each of this thread's butterflies one step ahead: the
-      // registers of butterfly i are refilled with step t-1 as soon as step t
-      // has consumed them.
-      float pf[kPair ? UPT : 1][R], pfu[kPair ? UPT : 1][R];
+      // The next two butterflies in consumption order (t descending, i
+      // ascending).
+      float pa[R], pua[R], pb[R], pub[R];
       if constexpr (kPair) {
-#pragma unroll
-        for (int i = 0; i < UPT; ++i) {
-          load_vec<R>(slot_src(N - 1, i), pf[i]);
-          load_vec<R>(slot_src(N - 1, i) + R, pfu[i]);
+        load_vec<R>(slot_src(N - 1, 0), pa);
+        load_vec<R>(slot_src(N - 1, 0) + R, pua);
+        if (UPT > 1 || N > 1) {
+          const float* src = UPT > 1 ? slot_src(N - 1, 1) : slot_src(N - 2, 0);
+          load_vec<R>(src, pb);
+          load_vec<R>(src + R, pub);
         }
       }
       double D = 0.0;  // D_t
@@ -350,15 +377,20 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
         // inputs nr[c] (maximum 0) and raw nu inputs, and the butterfly's
         // contribution to the gradient sums (a0 for sum dll, a1 for sum dll h).
         // pms = raw m~_{t-1}(p*NB + u) + Kt - sh.  Returns the group sum.
-        auto beta_out = [&](auto shift_tag, int p, uint32_t xu, int u, const float (&nr)[R],
+        auto beta_out = [&](auto shift_tag, int i, int p, uint32_t xu, int u, const float (&nr)[R],
                             const float (&nui)[R], float pms, float pmu, float oout, float& no, float& nuo,
                             float& a0, float (&a1)[V]) -> float {
           constexpr bool SHIFT = decltype(shift_tag)::value;
           float y[R], z[R], hh[R][V];
 #pragma unroll
           for (int c = 0; c < R; ++c) {
-            raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)c, (uint32_t)(p * NT + R * u + c), P.table,
-                                  lut, P.Q, hh[c]);
+            if (i < CU) {
+#pragma unroll
+              for (int v = 0; v < V; ++v) hh[c][v] = hc[i < CU ? i : 0][p][c][v];
+            } else {
+              raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)c, (uint32_t)(p * NT + R * u + c), P.table,
+                                    lut, P.Q, hh[c]);
+            }
             float yy = nr[c];
             float zz = nui[c];
 #pragma unroll
@@ -421,21 +453,25 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
 #pragma unroll
           for (int r = 0; r < R; ++r) {
             if constexpr (kPair) {
-              pm[r] = pf[i][r];
-              pmu[r] = pfu[i][r];
+              pm[r] = pa[r];
+              pmu[r] = pua[r];
+              pa[r] = pb[r];
+              pua[r] = pub[r];
             }
             ni[r] = nx[r];
             nui[r] = nxu[r];
           }
-          if constexpr (kPair) {
-            if (t > 0) {
-              load_vec<R>(slot_src(t - 1, i), pf[i]);
-              load_vec<R>(slot_src(t - 1, i) + R, pfu[i]);
+          if constexpr (kPair) {  // fetch the butterfly two ahead
+            const int tt = i + 2 < UPT ? t : t - 1 - (i + 2 - UPT) / UPT;
+            const int ii = i + 2 < UPT ? i + 2 : (i + 2 - UPT) % UPT;
+            if (tt >= 0) {
+              load_vec<R>(slot_src(tt, ii), pb);
+              load_vec<R>(slot_src(tt, ii) + R, pub);
             }
           }
           if (i + 1 < UPT) read_in(i + 1, nx, nxu);
           if (q < NB) {
-            const int u = opaque(q);
+            const int u = i < CU ? q : opaque(q);
             float Mu = ni[0];
 #pragma unroll
             for (int c = 1; c < R; ++c) Mu = fmaxf(Mu, ni[c]);
@@ -454,7 +490,7 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
 #pragma unroll
               for (int p = 0; p < R; ++p) {
                 float a0, a1[V];
-                const float s = beta_out(Fast{}, p, xu, u, nr, nui, pm[p] + kts, pmu[p], oout, no[p], nuo[p], a0, a1);
+                const float s = beta_out(Fast{}, i, p, xu, u, nr, nui, pm[p] + kts, pmu[p], oout, no[p], nuo[p], a0, a1);
                 smin = p ? fminf(smin, s) : s;
                 ua0 += a0;
 #pragma unroll
@@ -468,7 +504,7 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
 #pragma unroll
                   for (int p = 0; p < R; ++p) {
                     float a0, a1[V];
-                    beta_out(std::true_type{}, p, xu, u, nr, nui, pm[p] + kts, pmu[p], oout, no[p], nuo[p], a0, a1);
+                    beta_out(std::true_type{}, i, p, xu, u, nr, nui, pm[p] + kts, pmu[p], oout, no[p], nuo[p], a0, a1);
                     ua0 += a0;
 #pragma unroll
                     for (int v = 0; v < V; ++v) ua1[v] += a1[v];
@@ -489,9 +525,9 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
               for (int p = 0; p < R; ++p) {
                 float no, nuo, a0, a1[V];
                 const float pms = src[p] + kts, pmup = src[R + p];
-                const float s = beta_out(Fast{}, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
+                const float s = beta_out(Fast{}, i, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
                 if (!EXACT && s < kUnderflow)
-                  beta_out(std::true_type{}, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
+                  beta_out(std::true_type{}, i, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
                 A0 += a0;
 #pragma unroll
                 for (int v = 0; v < V; ++v) A1[v] += a1[v];
@@ -536,9 +572,10 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
   }
 }
 
-#define BCJR_BWD_CASE(KV_, V_, CODE_, UPT_) \
-  if (KV == KV_ && V == V_ && code == CODE_ && upt == UPT_) \
-    return reinterpret_cast<const void*>(&bcjr_bwd_kernel<KV_, V_, CODE_, UPT_>);
+#define BCJR_BWD_CASE(KV_, V_, CODE_, UPT_)                                                  \
+  if (KV == KV_ && V == V_ && code == CODE_ && upt == UPT_)                                 \
+    return reinterpret_cast<const void*>(                                                   \
+        &bcjr_bwd_kernel<KV_, V_, CODE_, UPT_, bwd_cached_units(KV_, V_, UPT_)>);
 
 #define BCJR_BWD_UPTS(KV_, V_, CODE_) \
   BCJR_BWD_CASE(KV_, V_, CODE_, 1)    \
@@ -553,7 +590,7 @@ const void* bwd_kernel_ptr(int KV, int V, int code, int upt) {
   BCJR_BWD_UPTS(2, 1, CODE_3INST)
   BCJR_BWD_UPTS(2, 2, CODE_TABLE)
   BCJR_BWD_UPTS(2, 2, CODE_HYB)
-  // kV = 4: whole 16-way butterflies, at most 256 per sequence (L <= 16).
+  // kV = 4: whole 16-state butterflies, at most 256 per sequence (L <= 16).
   BCJR_BWD_CASE(4, 1, CODE_TABLE, 1)
   BCJR_BWD_CASE(4, 1, CODE_1MAD, 1)
   BCJR_BWD_CASE(4, 1, CODE_3INST, 1)

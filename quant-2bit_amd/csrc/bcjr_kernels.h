@@ -22,6 +22,14 @@ constexpr int fwd_cached_units(int KV, int V, int upt) {
                                                                         : kFwdCacheVgprs / ((1 << KV) * (1 << KV) * V));
 }
 
+// The same budget for the backward.
+constexpr int kBwdCacheVgprs = 64;
+constexpr int bwd_cached_units(int KV, int V, int upt) {
+  return KV >= 4 ? 0
+                 : (upt < kBwdCacheVgprs / ((1 << KV) * (1 << KV) * V) ? upt
+                                                                        : kBwdCacheVgprs / ((1 << KV) * (1 << KV) * V));
+}
+
 const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool internals);
 const void* bwd_kernel_ptr(int KV, int V, int code, int upt);
 const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache);
