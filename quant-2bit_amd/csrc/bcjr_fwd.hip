@@ -244,19 +244,17 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
       __syncthreads();
 
       // ------------------------------ beta sweep -------------------------------
-      // Raw alpha inputs of step t come back from HBM one step ahead of their
-      // use.
+      // Raw alpha inputs of step t come back from HBM two butterflies ahead of
+      // their use, across step boundaries (the next two in consumption order:
+      // t descending, i ascending).
       auto slot_src = [&](int t, int i) {
         const int q = min(tid + i * nthr, NB - 1);
         return slot + ((size_t)t * NB + q) * R;
       };
-      // Slot inputs of each of this thread's butterflies one step ahead: the
-      // register set of butterfly i is refilled with step t-1 as soon as
-      // step t has consumed it.
-      float pf[kPair ? UPT : 1][R];
+      float pa[R], pb[R];
       if constexpr (kPair) {
-#pragma unroll
-        for (int i = 0; i < UPT; ++i) load_vec<R>(slot_src(N - 1, i), pf[i]);
+        load_vec<R>(slot_src(N - 1, 0), pa);
+        if (UPT > 1 || N > 1) load_vec<R>(UPT > 1 ? slot_src(N - 1, 1) : slot_src(N - 2, 0), pb);
       }
       double D = 0.0;  // D_t
       for (int t = N - 1; t >= 0; --t, ++k) {
@@ -344,10 +342,15 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 #pragma unroll
           for (int r = 0; r < R; ++r) {
             n[r] = nx[r];
-            if constexpr (kPair) pm[r] = pf[i][r];
+            if constexpr (kPair) {
+              pm[r] = pa[r];
+              pa[r] = pb[r];
+            }
           }
-          if constexpr (kPair) {
-            if (t > 0) load_vec<R>(slot_src(t - 1, i), pf[i]);
+          if constexpr (kPair) {  // fetch the butterfly two ahead
+            const int tt = i + 2 < UPT ? t : t - 1 - (i + 2 - UPT) / UPT;
+            const int ii = i + 2 < UPT ? i + 2 : (i + 2 - UPT) % UPT;
+            if (tt >= 0) load_vec<R>(slot_src(tt, ii), pb);
           }
           if (i + 1 < UPT) read_in(i + 1, nx);
           if (q < NB) {

@@ -15,7 +15,7 @@ struct VitParams;
 // Butterflies per thread (of upt) whose codewords the soft forward keeps in
 // VGPRs for the whole launch: as many as fit kFwdCacheVgprs (R*R*V each);
 // 16-state butterflies are never cached.
-constexpr int kFwdCacheVgprs = 64;
+constexpr int kFwdCacheVgprs = 96;
 constexpr int fwd_cached_units(int KV, int V, int upt) {
   return KV >= 4 ? 0
                  : (upt < kFwdCacheVgprs / ((1 << KV) * (1 << KV) * V) ? upt
