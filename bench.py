@@ -15,8 +15,10 @@ Also reported:
     gradient);
   * HBM bytes per step from the committed counter summary
     (profiles/bcjr_tile_hbm_traffic.txt), when present;
-  * seconds per Llama-3.2-1B decoder-layer QAT step (237,568 sequences), from a
-    4,096-sequence batch timed at each per-tensor temperature of that layer;
+  * seconds per Llama-3.2-1B decoder-layer QAT step (237,568 sequences): a
+    4,096-sequence fwd+bwd timed at each per-tensor temperature of that layer,
+    plus the Viterbi pack of every tile and the random Hadamard transforms
+    around each weight tensor;
   * the CPU oracle (C/OpenMP) timed on a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--config tile|cpu]
@@ -267,11 +269,43 @@ def layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev):
         sec = e0.elapsed_time(e1) / 1e3 * (rows * cols // 256) / B
         per[name] = {"T": T, "sequences": rows * cols // 256, "seconds": sec}
         total += sec
+    # The T -> 0 Viterbi pack of every tile (walks, 2-bit bitstream) after the soft pass.
+    _, table = bcjr.forward_backward._spec_for(cb, L, k, V)
+    ops.viterbi(spec, x, table)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    ops.viterbi(spec, x, table)
+    e1.record(stream)
+    torch.cuda.synchronize(dev)
+    vit_batch_s = e0.elapsed_time(e1) / 1e3
+    vit = vit_batch_s * LAYER_SEQS / B
+    # Random Hadamard transforms around each tensor's quantizer: RHT and its
+    # inverse in the forward, their adjoints (the same two transforms) in the
+    # backward.  Algorithmic bytes: one read and one write of the matrix.
+    rht_s, rht_rates = 0.0, {}
+    for name, rows, cols, _ in LAYER_TENSORS:
+        Wm = torch.randn(rows, cols, device=dev)
+        sl = torch.ones(rows, device=dev)
+        sr = torch.ones(cols, device=dev)
+        bcjr.apply_inverse_rht_gpu(bcjr.apply_rht_gpu(Wm, sl, sr), sl, sr)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        Wt = bcjr.apply_rht_gpu(Wm, sl, sr)
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        one = e0.elapsed_time(e1) / 1e3
+        rht_s += 4 * one
+        rht_rates[name] = {"ms": one * 1e3, "GB_s": 8.0 * rows * cols / one / 1e9}
+        del Wt
     cells = float(LAYER_SEQS) * N * (1 << L)
-    return {"seconds": total, "sequences": LAYER_SEQS, "tensors": per,
+    return {"seconds": total + vit + rht_s, "soft_seconds": total, "viterbi_seconds": vit,
+            "rht_seconds": rht_s, "rht_per_tensor": rht_rates,
+            "viterbi_ms_per_%d_sequences" % B: vit_batch_s * 1e3,
+            "sequences": LAYER_SEQS, "tensors": per,
             "state_updates_per_s": 4.0 * cells / total,
             "note": "fwd+bwd per tensor timed on a %d-sequence batch at that tensor's T, scaled by its "
-                    "sequence count" % B}
+                    "sequence count, plus one Viterbi pack of every tile and four random Hadamard "
+                    "transforms per tensor" % B}
 
 
 def calibration_copy(torch, dev):

@@ -19,6 +19,9 @@
  *                  src/qat/ste.py:270-283 (_replay_walks)
  *   bcjr_codebook  src/codes/ref.py:33-41,76-91 (1MAD, 3INST) and
  *                  src/qat/ste.py:376-392 (make_hyb_codebook_gpu)
+ *   bcjr_hadamard  fast_hadamard_transform.hadamard_transform (src/rht/transform.py:44-55)
+ *   bcjr_rht       src/qat/ste.py:113-135 (apply_rht_gpu, apply_inverse_rht_gpu),
+ *                  src/rht/transform.py:65-126
  *
  * Conventions
  *   - All pointers are device pointers owned by the caller; inputs are read-only.
@@ -137,6 +140,25 @@ int bcjr_decode(const bcjr_problem* prob, const int32_t* bitstream, const uint8_
  * reference generators. */
 int bcjr_codebook(const bcjr_problem* prob, const float* lut, float* codebook_out,
                   hipStream_t stream);
+
+/* Fast Walsh-Hadamard transform of each row of a (rows, n) float32 matrix:
+ * out[r, :] = scale * H_n x[r, :] with H_n the unscaled Sylvester Hadamard
+ * matrix, butterflies in the order of fwht_numpy (src/rht/transform.py:26-42).
+ * n a power of two, 1 <= n <= 16384; out may equal x.  Replaces
+ * fast_hadamard_transform.hadamard_transform as called by src/rht/transform.py:44-55
+ * and src/qat/ste.py:113-135. */
+int bcjr_hadamard(const float* x, float* out, int64_t rows, int64_t n, float scale,
+                  hipStream_t stream);
+
+/* Random Hadamard transform of an (m, n) float32 matrix W (m, n powers of two,
+ * 1 <= m <= 16384, 64 <= n <= 16384), sign vectors sign_l (m) and sign_r (n):
+ *   inverse = 0: out = H_m diag(sign_l) W diag(sign_r) H_n / sqrt(m*n)
+ *   inverse = 1: out = diag(sign_l) H_m W H_n diag(sign_r) / sqrt(m*n)
+ * out must not alias W.  Replaces apply_rht_gpu / apply_inverse_rht_gpu
+ * (src/qat/ste.py:113-135) and apply_rht / apply_inverse_rht
+ * (src/rht/transform.py:65-126). */
+int bcjr_rht(const float* W, float* out, int64_t m, int64_t n, const float* sign_l,
+             const float* sign_r, int inverse, hipStream_t stream);
 
 /* Static name of a status code. */
 const char* bcjr_strerror(int status);

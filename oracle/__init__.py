@@ -21,8 +21,26 @@ Contents
                           their form.
 ``pack_bits / unpack_bits``
                           2-bit (k*V-bit) LSB-first packing of per-step indices.
+``fwht / rht / inverse_rht``
+                          the random Hadamard transform of src/rht/transform.py.
 
-Parity status of each restatement is listed in ``oracle/PINNING.md``.
+How each restatement is pinned (tests/test_oracle.py)
+-----------------------------------------------------
+bcjr_forward / bcjr_backward   brute-force path enumeration on tiny trellises (itself
+                               checked by finite differences of log Z and soft), the
+                               gather form ``naive_forward``, T -> inf / T -> 0 limits,
+                               linearity of the gradient in g.
+viterbi / decode               the L=2 known answer of the reference's
+                               test_viterbi.py:17-53, brute-force minimum-cost paths,
+                               tie rules, the 1MAD Table-1 MSE band, round trips.
+codebook                       golden vectors written from src/codes/ref.py
+                               (tests/golden/code_vectors.json).
+pack_bits / unpack_bits        round trips and hand-checked byte layouts.
+fwht / rht / inverse_rht       scipy.linalg.hadamard (Sylvester) matrix products,
+                               bit-exact on integer inputs; rht . inverse_rht = I;
+                               norm preservation.
+No function is parity unpinned.  What no check here can pin is the reference's
+own float32 rounding of its eager torch ops (no fixtures of it exist).
 """
 from __future__ import annotations
 
@@ -308,3 +326,49 @@ def unpack_bits(packed, N, KV):
     per = 8 // KV
     t = np.arange(N)
     return ((packed[:, t // per] >> ((t % per) * KV)) & ((1 << KV) - 1)).astype(np.int32)
+
+
+# ---------------------------------------------------------------------------
+# Random Hadamard transform (src/rht/transform.py)
+# ---------------------------------------------------------------------------
+def fwht(x):
+    """Unscaled fast Walsh-Hadamard transform on the last axis in float32, with the
+    butterflies of fwht_numpy (src/rht/transform.py:26-42): h = 1, 2, 4, ...,
+    x[i] = a + b, x[i+h] = a - b.  Vectorised over the blocks of each stage; the
+    arithmetic per element is the same."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    n = x.shape[-1]
+    assert n > 0 and n & (n - 1) == 0, n
+    h = 1
+    while h < n:
+        v = x.reshape(x.shape[:-1] + (n // (2 * h), 2, h))
+        a = v[..., 0, :].copy()
+        b = v[..., 1, :].copy()
+        v[..., 0, :] = a + b
+        v[..., 1, :] = a - b
+        h *= 2
+    return x
+
+
+def _rht_scale(W, m, n):
+    # float32 result of dividing by sqrt(m*n) in float64, as the reference's
+    # numpy path does (src/rht/transform.py:90-96)
+    return (W.astype(np.float64) / np.sqrt(m * n)).astype(np.float32)
+
+
+def rht(W, sign_l, sign_r):
+    """H_m diag(sl) W diag(sr) H_n / sqrt(m n)  (src/rht/transform.py:65-96)."""
+    W = np.asarray(W, dtype=np.float32)
+    m, n = W.shape
+    Wr = fwht(W * np.asarray(sign_r, np.float32)[None, :])
+    Wl = fwht((Wr * np.asarray(sign_l, np.float32)[:, None]).T).T
+    return _rht_scale(Wl, m, n)
+
+
+def inverse_rht(W_tilde, sign_l, sign_r):
+    """diag(sl) H_m W~ H_n diag(sr) / sqrt(m n)  (src/rht/transform.py:99-126)."""
+    W = np.asarray(W_tilde, dtype=np.float32)
+    m, n = W.shape
+    Wr = fwht(W) * np.asarray(sign_r, np.float32)[None, :]
+    Wl = fwht(Wr.T).T * np.asarray(sign_l, np.float32)[:, None]
+    return _rht_scale(Wl, m, n)

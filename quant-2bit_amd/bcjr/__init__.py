@@ -12,8 +12,9 @@ from .viterbi import (  # noqa: F401
     viterbi_decode_v_batched, viterbi_encode_chunked, viterbi_encode_v_batched_hip,
 )
 from .quant import (  # noqa: F401
-    bcjr_quantize_tiles, bcjr_quantize_weight_rotated, tile_for_viterbi, untile_from_viterbi,
+    bcjr_quantize_tiles, bcjr_quantize_weight, bcjr_quantize_weight_rotated, tile_for_viterbi, untile_from_viterbi,
 )
+from .rht import apply_inverse_rht_gpu, apply_rht_gpu, hadamard_transform, make_sign_vector  # noqa: F401
 from ._lib import LIB_PATH, load as load_library  # noqa: F401
 
 __version__ = "0.1.0"

@@ -4,14 +4,15 @@ Tiling follows src/qat/ste.py:138-159: an (m, n) matrix becomes
 (n_col_blocks * n_row_blocks) sequences of Tx*Ty weights, block index
 col_block * n_row_blocks + row_block, each 16x16 tile flattened row-major, then
 viewed as (B, N, V) with N = Tx*Ty / V.  The RMS scale is detached
-(bcjr_quant.py:140).  RHT wrapping (bcjr_quantize_weight) is not part of this
-package.
+(bcjr_quant.py:140).  bcjr_quantize_weight wraps the rotated quantizer in the
+random Hadamard transform (bcjr_quant.py:159-178) on the gfx950 FWHT kernels.
 """
 from __future__ import annotations
 
 import torch
 
 from .forward_backward import K_BITS, L_BITS, V_DIM, bcjr_forward_backward
+from .rht import apply_inverse_rht_gpu, apply_rht_gpu
 
 TX = 16
 TY = 16
@@ -74,5 +75,16 @@ def bcjr_quantize_weight_rotated(W_rotated, codebook, T_temp, preds=None, succs=
     return W_q_unit * W_scale
 
 
+def bcjr_quantize_weight(W_latent, sign_l, sign_r, codebook, T_temp, preds=None, succs=None,
+                         chunk_size=BCJR_CHUNK, Tx=TX, Ty=TY, L=L_BITS, k=K_BITS, V=V_DIM):
+    """Soft-quantize W in its original basis: rotate, quantize, rotate back
+    (bcjr_quant.py:159-178).  Gradients flow through both transforms and the
+    BCJR node."""
+    W_tilde = apply_rht_gpu(W_latent, sign_l, sign_r)
+    W_tilde_q = bcjr_quantize_weight_rotated(W_tilde, codebook, T_temp, preds, succs, chunk_size=chunk_size,
+                                             Tx=Tx, Ty=Ty, L=L, k=k, V=V)
+    return apply_inverse_rht_gpu(W_tilde_q, sign_l, sign_r)
+
+
 __all__ = ["TX", "TY", "tile_for_viterbi", "untile_from_viterbi", "bcjr_quantize_tiles",
-           "bcjr_quantize_weight_rotated"]
+           "bcjr_quantize_weight_rotated", "bcjr_quantize_weight"]

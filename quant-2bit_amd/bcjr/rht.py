@@ -1,0 +1,108 @@
+"""Random Hadamard transform (RHT) around the BCJR quantizer, on gfx950 kernels.
+
+Drop-in for the GPU RHT of the reference:
+  * hadamard_transform(x, scale)  -- fast_hadamard_transform.hadamard_transform,
+    used by src/rht/transform.py:44-55 and src/qat/ste.py:113-135;
+  * apply_rht_gpu / apply_inverse_rht_gpu (src/qat/ste.py:113-135), which equal
+    apply_rht / apply_inverse_rht of src/rht/transform.py:65-126;
+  * make_sign_vector (src/rht/transform.py:58-62).
+
+RHT(W) = H_m diag(sl) W diag(sr) H_n / sqrt(m n) is linear and its adjoint is
+the inverse transform, so the autograd backward of each is the other one.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+
+
+def make_sign_vector(n, seed):
+    """Random +-1 float32 vector of length n (src/rht/transform.py:58-62): the same
+    generator and draw, so sign vectors saved with reference checkpoints match."""
+    rng = np.random.default_rng(seed)
+    return rng.choice([-1.0, 1.0], size=n).astype(np.float32)
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _hadamard(x: torch.Tensor, scale: float) -> torch.Tensor:
+    if not x.is_cuda or x.dtype != torch.float32:
+        raise AssertionError("hadamard_transform expects a float32 GPU tensor")
+    n = x.shape[-1]
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    rows = xc.numel() // n if n else 0
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.load().bcjr_hadamard(_lib.ptr(xc), _lib.ptr(out), rows, n, float(scale),
+                                             _stream(x.device)), "bcjr_hadamard")
+    return out
+
+
+class HadamardFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, scale):
+        ctx.scale = scale
+        return _hadamard(x, scale)
+
+    @staticmethod
+    def backward(ctx, g):  # H is symmetric
+        return _hadamard(g, ctx.scale), None
+
+
+def hadamard_transform(x: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """scale * H_n x along the last axis (unscaled Sylvester H_n, n a power of two)."""
+    return HadamardFunction.apply(x, scale)
+
+
+def _check_rht_args(W, sign_l, sign_r):
+    if W.dim() != 2 or not W.is_cuda or W.dtype != torch.float32:
+        raise AssertionError(f"W must be a 2-D float32 GPU tensor; got {tuple(W.shape)} {W.dtype}")
+    m, n = W.shape
+    if tuple(sign_l.shape) != (m,) or tuple(sign_r.shape) != (n,):
+        raise AssertionError(f"sign vectors must be ({m},) and ({n},); got {tuple(sign_l.shape)}, "
+                             f"{tuple(sign_r.shape)}")
+
+
+def _rht(W, sign_l, sign_r, inverse: bool) -> torch.Tensor:
+    _check_rht_args(W, sign_l, sign_r)
+    m, n = W.shape
+    Wc = W.detach().contiguous()
+    sl = sign_l.detach().to(device=W.device, dtype=torch.float32).contiguous()
+    sr = sign_r.detach().to(device=W.device, dtype=torch.float32).contiguous()
+    out = torch.empty_like(Wc)
+    with torch.cuda.device(W.device):
+        _lib.check(_lib.load().bcjr_rht(_lib.ptr(Wc), _lib.ptr(out), m, n, _lib.ptr(sl), _lib.ptr(sr),
+                                        1 if inverse else 0, _stream(W.device)), "bcjr_rht")
+    return out
+
+
+class RhtFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, W, sign_l, sign_r, inverse):
+        ctx.save_for_backward(sign_l, sign_r)
+        ctx.inverse = inverse
+        return _rht(W, sign_l, sign_r, inverse)
+
+    @staticmethod
+    def backward(ctx, g):  # the adjoint of the transform is its inverse
+        sign_l, sign_r = ctx.saved_tensors
+        return _rht(g.contiguous(), sign_l, sign_r, not ctx.inverse), None, None, None
+
+
+def apply_rht_gpu(W, sign_l_gpu, sign_r_gpu):
+    """W~ = H_m diag(sl) W diag(sr) H_n / sqrt(m n)  (src/qat/ste.py:113-126)."""
+    return RhtFunction.apply(W, sign_l_gpu, sign_r_gpu, False)
+
+
+def apply_inverse_rht_gpu(W_tilde, sign_l_gpu, sign_r_gpu):
+    """W = diag(sl) H_m W~ H_n diag(sr) / sqrt(m n)  (src/qat/ste.py:129-135)."""
+    return RhtFunction.apply(W_tilde, sign_l_gpu, sign_r_gpu, True)
+
+
+__all__ = ["make_sign_vector", "hadamard_transform", "apply_rht_gpu", "apply_inverse_rht_gpu"]

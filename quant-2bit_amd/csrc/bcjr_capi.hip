@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -464,6 +465,42 @@ int bcjr_codebook(const bcjr_problem* prob, const float* lut, float* codebook_ou
   hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, stream);
   if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel(codebook)");
   return BCJR_OK;
+}
+
+int bcjr_hadamard(const float* x, float* out, int64_t rows, int64_t n, float scale, hipStream_t stream) {
+  if (rows < 0) return fail(BCJR_EINVAL, "rows=%lld must be >= 0", (long long)rows);
+  if (n < 1 || n > 16384 || (n & (n - 1)))
+    return fail(BCJR_EINVAL, "n=%lld must be a power of two in [1, 16384]", (long long)n);
+  if (rows == 0) return BCJR_OK;
+  if (!x || !out) return fail(BCJR_EINVAL, "x and out must be non-NULL");
+  DeviceInfo di;
+  int rc = device_info(&di);
+  if (rc) return rc;
+  hipError_t e = bcjr::launch_fwht_rows(x, out, rows, (int)n, nullptr, nullptr, nullptr, scale, di.num_cu * 8,
+                                        stream);
+  return e == hipSuccess ? BCJR_OK : hip_fail(e, "bcjr_hadamard launch");
+}
+
+int bcjr_rht(const float* W, float* out, int64_t m, int64_t n, const float* sign_l, const float* sign_r,
+             int inverse, hipStream_t stream) {
+  if (m < 1 || m > 16384 || (m & (m - 1)))
+    return fail(BCJR_EINVAL, "m=%lld must be a power of two in [1, 16384]", (long long)m);
+  if (n < 64 || n > 16384 || (n & (n - 1)))
+    return fail(BCJR_EINVAL, "n=%lld must be a power of two in [64, 16384]", (long long)n);
+  if (!W || !out || !sign_l || !sign_r) return fail(BCJR_EINVAL, "W, out, sign_l and sign_r must be non-NULL");
+  if (W == out) return fail(BCJR_EINVAL, "out must not alias W");
+  DeviceInfo di;
+  int rc = device_info(&di);
+  if (rc) return rc;
+  const float s = (float)(1.0 / sqrt((double)m * (double)n));
+  const int blocks = di.num_cu * 8;
+  // forward: rows of W diag(sr) H_n, then row signs, then H_m and the scale;
+  // inverse: rows of W H_n then diag(sr), then H_m, row signs and the scale.
+  hipError_t e = inverse ? bcjr::launch_fwht_rows(W, out, m, (int)n, nullptr, sign_r, nullptr, 1.0f, blocks, stream)
+                         : bcjr::launch_fwht_rows(W, out, m, (int)n, sign_r, nullptr, sign_l, 1.0f, blocks, stream);
+  if (e != hipSuccess) return hip_fail(e, "bcjr_rht row pass");
+  e = bcjr::launch_fwht_cols(out, (int)m, (int)n, inverse ? sign_l : nullptr, s, blocks, stream);
+  return e == hipSuccess ? BCJR_OK : hip_fail(e, "bcjr_rht column pass");
 }
 
 const char* bcjr_strerror(int status) {

@@ -4,6 +4,7 @@
 // validation, occupancy and launch.
 #pragma once
 
+#include <hip/hip_runtime.h>
 #include <stddef.h>
 
 namespace bcjr {
@@ -35,6 +36,15 @@ const void* bwd_kernel_ptr(int KV, int V, int code, int upt);
 const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache);
 const void* decode_kernel_ptr(int KV, int V, int code);
 const void* codebook_kernel_ptr(int code);
+
+// Hadamard transforms (bcjr_rht.hip).  Rows: out[r] = scale * row_sign[r] *
+// post .* H_n (pre .* x[r]), n a power of two <= 16384, out may equal x.
+// Columns: x = scale * diag(row_sign) H_m x in place, m <= 16384, n % 64 == 0.
+hipError_t launch_fwht_rows(const float* x, float* out, long long rows, int n, const float* pre,
+                            const float* post, const float* row_sign, float scale, int max_blocks,
+                            hipStream_t stream);
+hipError_t launch_fwht_cols(float* x, int m, int n, const float* row_sign, float scale, int max_blocks,
+                            hipStream_t stream);
 
 // LDS bytes for one workgroup.
 inline size_t fwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {

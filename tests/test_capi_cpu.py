@@ -124,3 +124,38 @@ def test_python_surface_asserts_like_reference():
         bcjr_forward_backward(seq, torch.zeros(10, 2), 1.0, L=6, k=2, V=2)
     with pytest.raises(AssertionError):  # CPU tensors: the node runs only on the GPU
         bcjr_forward_backward(seq, cb, 1.0, L=6, k=2, V=2)
+
+
+@pytest.mark.parametrize("m,n,msg", [
+    (3, 64, "m=3"), (0, 64, "m=0"), (32768, 64, "m=32768"),
+    (64, 32, "n=32"), (64, 96, "n=96"), (64, 32768, "n=32768"),
+])
+def test_rht_validation_without_device(lib, m, n, msg):
+    dummy = ctypes.c_void_p(16)  # never dereferenced: the shape check fails first
+    assert lib.bcjr_rht(dummy, ctypes.c_void_p(32), m, n, dummy, dummy, 0, None) == -1
+    assert msg in lib.bcjr_last_error().decode()
+
+
+def test_rht_rejects_null_and_alias(lib):
+    p = ctypes.c_void_p(16)
+    assert lib.bcjr_rht(None, p, 64, 64, p, p, 0, None) == -1
+    assert "non-NULL" in lib.bcjr_last_error().decode()
+    assert lib.bcjr_rht(p, p, 64, 64, ctypes.c_void_p(32), ctypes.c_void_p(48), 1, None) == -1
+    assert "alias" in lib.bcjr_last_error().decode()
+
+
+def test_hadamard_validation_without_device(lib):
+    assert lib.bcjr_hadamard(None, None, 4, 48, 1.0, None) == -1
+    assert "n=48" in lib.bcjr_last_error().decode()
+    assert lib.bcjr_hadamard(None, None, -1, 64, 1.0, None) == -1
+    assert lib.bcjr_hadamard(None, None, 0, 64, 1.0, None) == 0   # nothing to do
+    assert lib.bcjr_hadamard(None, None, 2, 64, 1.0, None) == -1
+    assert "non-NULL" in lib.bcjr_last_error().decode()
+
+
+def test_sign_vector_generator_matches_reference_draw():
+    # src/rht/transform.py:58-62: default_rng(seed).choice([-1.0, 1.0], size=n) as float32
+    import bcjr
+    s = bcjr.make_sign_vector(1000, 7)
+    ref = np.random.default_rng(7).choice([-1.0, 1.0], size=1000).astype(np.float32)
+    assert s.dtype == np.float32 and np.array_equal(s, ref)

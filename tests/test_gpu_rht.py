@@ -1,0 +1,129 @@
+"""GPU parity of the Hadamard / RHT kernels against the oracle (src/rht/transform.py
+restated), and the RHT-wrapped quantizer (src/bcjr/bcjr_quant.py:159-178) against
+the oracle composition of transform, BCJR and inverse transform."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SOFT_TOL = 1e-4
+GRAD_TOL = 1e-3
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _signs(n, seed):
+    return np.random.default_rng(seed).choice([-1.0, 1.0], size=n).astype(np.float32)
+
+
+@pytest.mark.parametrize("rows,n", [(5, 1), (3, 2), (7, 64), (33, 256), (16, 2048), (4, 8192), (2, 16384)])
+def test_hadamard_bit_exact(bcjr_mod, oracle, rows, n):
+    _say(f"hadamard rows={rows} n={n}")
+    x = np.random.default_rng(n).standard_normal((rows, n)).astype(np.float32)
+    y = bcjr_mod.hadamard_transform(torch.tensor(x, device="cuda"))
+    assert np.array_equal(y.cpu().numpy(), oracle.fwht(x))
+    y2 = bcjr_mod.hadamard_transform(torch.tensor(x, device="cuda"), scale=0.25)
+    assert np.array_equal(y2.cpu().numpy(), oracle.fwht(x) * np.float32(0.25))
+
+
+def test_hadamard_batched_shape_and_grad(bcjr_mod, oracle):
+    _say("hadamard 3-D + grad")
+    x = torch.randn(2, 3, 128, device="cuda", requires_grad=True)
+    g = torch.randn(2, 3, 128, device="cuda")
+    y = bcjr_mod.hadamard_transform(x, scale=0.5)
+    (y * g).sum().backward()
+    assert y.shape == x.shape
+    assert np.array_equal(y.detach().cpu().numpy().reshape(6, 128),
+                          oracle.fwht(x.detach().cpu().numpy().reshape(6, 128)) * np.float32(0.5))
+    # H is symmetric: the gradient is the same transform of g
+    assert np.array_equal(x.grad.cpu().numpy().reshape(6, 128),
+                          oracle.fwht(g.cpu().numpy().reshape(6, 128)) * np.float32(0.5))
+
+
+# (m, n) with m*n an even power of two: the scale is exact and results are bit-exact
+EXACT = [(1, 64), (64, 64), (256, 256), (512, 2048), (2048, 512), (128, 8192), (16384, 64)]
+
+
+@pytest.mark.parametrize("m,n", EXACT)
+def test_rht_bit_exact(bcjr_mod, oracle, m, n):
+    _say(f"rht m={m} n={n}")
+    rng = np.random.default_rng(m + n)
+    W = rng.standard_normal((m, n)).astype(np.float32)
+    sl, sr = _signs(m, 1), _signs(n, 2)
+    Wt = bcjr_mod.apply_rht_gpu(torch.tensor(W, device="cuda"), torch.tensor(sl, device="cuda"),
+                                torch.tensor(sr, device="cuda"))
+    ref = oracle.rht(W, sl, sr)
+    assert np.array_equal(Wt.cpu().numpy(), ref)
+    back = bcjr_mod.apply_inverse_rht_gpu(Wt, torch.tensor(sl, device="cuda"), torch.tensor(sr, device="cuda"))
+    assert np.array_equal(back.cpu().numpy(), oracle.inverse_rht(ref, sl, sr))
+    assert np.abs(back.cpu().numpy() - W).max() <= 1e-5 * np.abs(W).max()
+
+
+@pytest.mark.parametrize("m,n", [(2, 64), (128, 256), (2048, 64)])
+def test_rht_odd_power_scale(bcjr_mod, oracle, m, n):
+    """m*n an odd power of two: 1/sqrt(mn) is inexact; float32 multiply vs the
+    reference's float64 division differ by at most one rounding."""
+    _say(f"rht odd m={m} n={n}")
+    W = np.random.default_rng(3).standard_normal((m, n)).astype(np.float32)
+    sl, sr = _signs(m, 4), _signs(n, 5)
+    Wt = bcjr_mod.apply_rht_gpu(torch.tensor(W, device="cuda"), torch.tensor(sl, device="cuda"),
+                                torch.tensor(sr, device="cuda")).cpu().numpy()
+    ref = oracle.rht(W, sl, sr)
+    assert np.abs(Wt - ref).max() <= 2 * np.spacing(np.abs(ref).max())
+
+
+def test_rht_adjoint_is_inverse(bcjr_mod):
+    """<RHT(W), G> = <W, RHT^-1(G)>, and autograd's gradient of RHT is RHT^-1."""
+    _say("rht adjoint")
+    m, n = 256, 512
+    W = torch.randn(m, n, device="cuda", dtype=torch.float32, requires_grad=True)
+    G = torch.randn(m, n, device="cuda")
+    sl = torch.tensor(_signs(m, 6), device="cuda")
+    sr = torch.tensor(_signs(n, 7), device="cuda")
+    Wt = bcjr_mod.apply_rht_gpu(W, sl, sr)
+    lhs = float((Wt.double() * G.double()).sum())
+    rhs = float((W.detach().double() * bcjr_mod.apply_inverse_rht_gpu(G, sl, sr).double()).sum())
+    assert abs(lhs - rhs) <= 1e-4 * max(1.0, abs(lhs))
+    (Wt * G).sum().backward()
+    assert torch.equal(W.grad, bcjr_mod.apply_inverse_rht_gpu(G, sl, sr))
+
+
+def test_quantize_weight_vs_oracle_composition(bcjr_mod, oracle):
+    """bcjr_quantize_weight (RHT -> RMS scale -> 16x16 tiles -> BCJR soft -> back) and its
+    gradient against the same steps on the oracle."""
+    _say("quantize_weight with RHT, L=12 1MAD T=0.1")
+    from bcjr.quant import tile_for_viterbi, untile_from_viterbi
+    L, k, V, T = 12, 2, 1, 0.1
+    m, n = 64, 256
+    rng = np.random.default_rng(11)
+    W = (rng.standard_normal((m, n)) * 0.02).astype(np.float32)
+    g = rng.standard_normal((m, n)).astype(np.float32)
+    sl, sr = _signs(m, 8), _signs(n, 9)
+    cb = bcjr_mod.make_1mad_codebook(L, "cuda")
+    cb_np = cb.cpu().numpy()
+    Wd = torch.tensor(W, device="cuda", requires_grad=True)
+    Wq = bcjr_mod.bcjr_quantize_weight(Wd, torch.tensor(sl, device="cuda"), torch.tensor(sr, device="cuda"),
+                                       cb, T, L=L, k=k, V=V)
+    (Wq * torch.tensor(g, device="cuda")).sum().backward()
+
+    # oracle composition
+    Wt = oracle.rht(W, sl, sr)
+    scale = np.float32(np.sqrt((Wt.astype(np.float32) ** 2).mean(dtype=np.float32)))
+    seqs, info = tile_for_viterbi(torch.tensor(Wt / scale), 16, 16)
+    seqs = seqs.numpy().reshape(seqs.shape[0], -1, V)
+    soft, _ = oracle.bcjr_forward(seqs, cb_np, T, L, k * V)
+    Wtq = untile_from_viterbi(torch.tensor(soft.reshape(seqs.shape[0], -1)), info, (m, n), 16, 16).numpy()
+    ref = oracle.inverse_rht(Wtq * scale, sl, sr)
+    got = Wq.detach().cpu().numpy()
+    assert np.abs(got - ref).max() <= SOFT_TOL * np.abs(ref).max()
+
+    # gradient: W_q = R^-1(s * U(soft(T(R(W)) / s))) with s detached
+    gt = oracle.rht(g, sl, sr)  # adjoint of R^-1 is R
+    gt_tiles, _ = tile_for_viterbi(torch.tensor(gt * scale), 16, 16)
+    d_seq = oracle.bcjr_backward(seqs, cb_np, T, L, k * V, gt_tiles.numpy().reshape(seqs.shape))
+    d_wt = untile_from_viterbi(torch.tensor(d_seq.reshape(seqs.shape[0], -1) / scale), info, (m, n), 16, 16).numpy()
+    grad_ref = oracle.inverse_rht(d_wt, sl, sr)  # adjoint of R is R^-1
+    assert np.abs(Wd.grad.cpu().numpy() - grad_ref).max() <= GRAD_TOL * np.abs(grad_ref).max()

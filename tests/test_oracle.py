@@ -207,3 +207,45 @@ def test_pack_roundtrip(oracle):
     for KV in (1, 2, 4):
         bits = rng.integers(0, 1 << KV, size=(5, 37)).astype(np.int32)
         assert (oracle.unpack_bits(oracle.pack_bits(bits, KV), 37, KV) == bits).all()
+
+
+def test_pack_layout_known_bytes(oracle):
+    # LSB-first: step t occupies bits [t*kV, (t+1)*kV) of the stream
+    bits = np.array([[1, 2, 3, 0, 3]], dtype=np.int32)
+    assert oracle.pack_bits(bits, 2).tolist() == [[1 | 2 << 2 | 3 << 4 | 0 << 6, 3]]
+    bits1 = np.array([[1, 0, 1, 1, 0, 0, 0, 1, 1]], dtype=np.int32)
+    assert oracle.pack_bits(bits1, 1).tolist() == [[0b10001101, 0b1]]
+    bits4 = np.array([[0xA, 0x3, 0xF]], dtype=np.int32)
+    assert oracle.pack_bits(bits4, 4).tolist() == [[0x3A, 0x0F]]
+
+
+# ---------------------------- Hadamard transform -----------------------------
+
+@pytest.mark.parametrize("n", [1, 2, 8, 64, 512])
+def test_fwht_is_sylvester_hadamard_product(oracle, n):
+    from scipy.linalg import hadamard
+    rng = np.random.default_rng(n)
+    Hm = hadamard(n).astype(np.float64)
+    xi = rng.integers(-50, 50, size=(3, n)).astype(np.float32)  # integer sums are exact in float32
+    assert np.array_equal(oracle.fwht(xi), (xi.astype(np.float64) @ Hm.T).astype(np.float32))
+    xf = rng.standard_normal((3, n)).astype(np.float32)
+    ref = xf.astype(np.float64) @ Hm.T
+    assert np.abs(oracle.fwht(xf) - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("m,n", [(4, 8), (64, 32), (16, 256)])
+def test_rht_matches_matrix_form_and_inverts(oracle, m, n):
+    from scipy.linalg import hadamard
+    rng = np.random.default_rng(m * n)
+    W = rng.standard_normal((m, n)).astype(np.float32)
+    sl = rng.choice([-1.0, 1.0], size=m).astype(np.float32)
+    sr = rng.choice([-1.0, 1.0], size=n).astype(np.float32)
+    Hm, Hn = hadamard(m).astype(np.float64), hadamard(n).astype(np.float64)
+    ref = Hm @ np.diag(sl) @ W.astype(np.float64) @ np.diag(sr) @ Hn / np.sqrt(m * n)
+    Wt = oracle.rht(W, sl, sr)
+    assert np.abs(Wt - ref).max() <= 1e-5 * np.abs(ref).max()
+    inv_ref = np.diag(sl) @ Hm @ ref @ Hn @ np.diag(sr) / np.sqrt(m * n)
+    assert np.abs(inv_ref - W).max() <= 1e-9 * np.abs(W).max() + 1e-12   # the matrix form itself inverts
+    back = oracle.inverse_rht(Wt, sl, sr)
+    assert np.abs(back - W).max() <= 1e-5 * np.abs(W).max()
+    assert abs(np.linalg.norm(Wt) - np.linalg.norm(W)) <= 1e-5 * np.linalg.norm(W)  # orthogonal
