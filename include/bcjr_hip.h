@@ -151,7 +151,7 @@ int bcjr_hadamard(const float* x, float* out, int64_t rows, int64_t n, float sca
                   hipStream_t stream);
 
 /* Random Hadamard transform of an (m, n) float32 matrix W (m, n powers of two,
- * 1 <= m <= 16384, 64 <= n <= 16384), sign vectors sign_l (m) and sign_r (n):
+ * 1 <= m, n <= 16384), sign vectors sign_l (m) and sign_r (n):
  *   inverse = 0: out = H_m diag(sign_l) W diag(sign_r) H_n / sqrt(m*n)
  *   inverse = 1: out = diag(sign_l) H_m W H_n diag(sign_r) / sqrt(m*n)
  * out must not alias W.  Replaces apply_rht_gpu / apply_inverse_rht_gpu

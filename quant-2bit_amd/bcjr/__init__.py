@@ -15,6 +15,10 @@ from .quant import (  # noqa: F401
     bcjr_quantize_tiles, bcjr_quantize_weight, bcjr_quantize_weight_rotated, tile_for_viterbi, untile_from_viterbi,
 )
 from .rht import apply_inverse_rht_gpu, apply_rht_gpu, hadamard_transform, make_sign_vector  # noqa: F401
+from .ste import (  # noqa: F401
+    TrellisQuantSTE, TrellisQuantSTE_IP, ptq_residual, quantize_forward_gpu, quantize_forward_gpu_no_rht,
+    replay_walks,
+)
 from ._lib import LIB_PATH, load as load_library  # noqa: F401
 
 __version__ = "0.1.0"

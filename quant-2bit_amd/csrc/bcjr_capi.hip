@@ -485,8 +485,8 @@ int bcjr_rht(const float* W, float* out, int64_t m, int64_t n, const float* sign
              int inverse, hipStream_t stream) {
   if (m < 1 || m > 16384 || (m & (m - 1)))
     return fail(BCJR_EINVAL, "m=%lld must be a power of two in [1, 16384]", (long long)m);
-  if (n < 64 || n > 16384 || (n & (n - 1)))
-    return fail(BCJR_EINVAL, "n=%lld must be a power of two in [64, 16384]", (long long)n);
+  if (n < 1 || n > 16384 || (n & (n - 1)))
+    return fail(BCJR_EINVAL, "n=%lld must be a power of two in [1, 16384]", (long long)n);
   if (!W || !out || !sign_l || !sign_r) return fail(BCJR_EINVAL, "W, out, sign_l and sign_r must be non-NULL");
   if (W == out) return fail(BCJR_EINVAL, "out must not alias W");
   DeviceInfo di;

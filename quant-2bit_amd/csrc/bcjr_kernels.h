@@ -39,7 +39,7 @@ const void* codebook_kernel_ptr(int code);
 
 // Hadamard transforms (bcjr_rht.hip).  Rows: out[r] = scale * row_sign[r] *
 // post .* H_n (pre .* x[r]), n a power of two <= 16384, out may equal x.
-// Columns: x = scale * diag(row_sign) H_m x in place, m <= 16384, n % 64 == 0.
+// Columns: x = scale * diag(row_sign) H_m x in place, m, n <= 16384 powers of two.
 hipError_t launch_fwht_rows(const float* x, float* out, long long rows, int n, const float* pre,
                             const float* post, const float* row_sign, float scale, int max_blocks,
                             hipStream_t stream);

@@ -12,7 +12,8 @@
 // Columns (first axis, stride n): m = a*b with b = min(m, 128); a first pass does
 // the stages h < b on tiles of b consecutive rows x 64 consecutive columns, a
 // second the stages h >= b on tiles of a rows spaced b apart; every global access
-// reads or writes 256 contiguous bytes of a row.  No transposes.
+// reads or writes 256 contiguous bytes of a row (4n bytes when n < 64).  No
+// transposes.
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
@@ -24,7 +25,7 @@ namespace bcjr {
 namespace {
 
 constexpr int kRowThreads = 256;
-constexpr int kColTile = 64;  // columns per column-pass tile
+constexpr int kColTile = 64;  // columns per column-pass tile (fewer when n < 64)
 constexpr int kColThreads = 256;
 
 // One butterfly stage of span h on n values in LDS: pairs (i, i + h) with
@@ -74,6 +75,7 @@ __global__ __launch_bounds__(kRowThreads) void fwht_rows_kernel(RowsParams P) {
 struct ColsParams {
   float* x;               // (m, n) transformed in place
   int n;
+  int C;                  // tile width: min(kColTile, n), a power of two dividing n
   int len;                // transform length along the column (tile rows)
   long long step;         // floats between consecutive tile rows
   long long outer_stride; // floats between tiles of consecutive outer index
@@ -84,32 +86,33 @@ struct ColsParams {
 };
 
 __global__ __launch_bounds__(kColThreads) void fwht_cols_kernel(ColsParams P) {
-  extern __shared__ __align__(16) float t[];  // len x kColTile
+  extern __shared__ __align__(16) float t[];  // len x C
   const int tid = threadIdx.x, nthr = blockDim.x;
-  const int ncb = P.n / kColTile;
+  const int C = P.C;
+  const int ncb = P.n / C;
   const long long tiles = (long long)P.outer * ncb;
   for (long long g = blockIdx.x; g < tiles; g += gridDim.x) {
     const int o = (int)(g / ncb), cb = (int)(g % ncb);
-    float* base = P.x + (size_t)o * P.outer_stride + (size_t)cb * kColTile;
-    for (int e = tid; e < P.len * kColTile; e += nthr) {
-      const int p = e / kColTile, c = e % kColTile;
+    float* base = P.x + (size_t)o * P.outer_stride + (size_t)cb * C;
+    for (int e = tid; e < P.len * C; e += nthr) {
+      const int p = e / C, c = e % C;
       t[e] = base[(size_t)p * P.step + c];
     }
     __syncthreads();
     // Stage h along the tile rows for every column: butterfly (p, p + h) of
-    // column c is item j = q * kColTile + c, q < len/2.
+    // column c is item j = q * C + c, q < len/2.
     for (int h = 1; h < P.len; h <<= 1) {
-      for (int j = tid; j < (P.len >> 1) * kColTile; j += nthr) {
-        const int q = j / kColTile, c = j % kColTile;
+      for (int j = tid; j < (P.len >> 1) * C; j += nthr) {
+        const int q = j / C, c = j % C;
         const int p = ((q & ~(h - 1)) << 1) | (q & (h - 1));
-        const float a = t[p * kColTile + c], b = t[(p + h) * kColTile + c];
-        t[p * kColTile + c] = a + b;
-        t[(p + h) * kColTile + c] = a - b;
+        const float a = t[p * C + c], b = t[(p + h) * C + c];
+        t[p * C + c] = a + b;
+        t[(p + h) * C + c] = a - b;
       }
       __syncthreads();
     }
-    for (int e = tid; e < P.len * kColTile; e += nthr) {
-      const int p = e / kColTile, c = e % kColTile;
+    for (int e = tid; e < P.len * C; e += nthr) {
+      const int p = e / C, c = e % C;
       float y = t[e];
       if (P.row_sign) y *= P.row_sign[o * P.row_o + p * P.row_p];
       base[(size_t)p * P.step + c] = y * P.scale;
@@ -136,27 +139,28 @@ hipError_t launch_fwht_rows(const float* x, float* out, long long rows, int n, c
 }
 
 // H_m applied to every column of the (m, n) matrix x, in place; the result is
-// multiplied by row_sign (after the transform) and scale.  n % 64 == 0.
+// multiplied by row_sign (after the transform) and scale.  m, n powers of two.
 hipError_t launch_fwht_cols(float* x, int m, int n, const float* row_sign, float scale, int max_blocks,
                             hipStream_t stream) {
   const int b = m < 128 ? m : 128;
   const int a = m / b;
+  const int C = n < kColTile ? n : kColTile;
   // pass 1: stages h < b, tiles of b consecutive rows
-  ColsParams P1 = {x, n, b, n, (long long)b * n, a, nullptr, 0, 0, 1.0f};
+  ColsParams P1 = {x, n, C, b, n, (long long)b * n, a, nullptr, 0, 0, 1.0f};
   if (a == 1) {  // the only pass: signs and scale here
     P1.row_sign = row_sign;
     P1.row_o = 0;
     P1.row_p = 1;
     P1.scale = scale;
   }
-  hipLaunchKernelGGL(fwht_cols_kernel, dim3(grid_for((long long)a * (n / kColTile), max_blocks)),
-                     dim3(kColThreads), (size_t)b * kColTile * sizeof(float), stream, P1);
+  hipLaunchKernelGGL(fwht_cols_kernel, dim3(grid_for((long long)a * (n / C), max_blocks)), dim3(kColThreads),
+                     (size_t)b * C * sizeof(float), stream, P1);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a == 1) return e;
   // pass 2: stages h >= b, tiles of a rows spaced b apart (row = ia*b + ib)
-  ColsParams P2 = {x, n, a, (long long)b * n, n, b, row_sign, 1, b, scale};
-  hipLaunchKernelGGL(fwht_cols_kernel, dim3(grid_for((long long)b * (n / kColTile), max_blocks)),
-                     dim3(kColThreads), (size_t)a * kColTile * sizeof(float), stream, P2);
+  ColsParams P2 = {x, n, C, a, (long long)b * n, n, b, row_sign, 1, b, scale};
+  hipLaunchKernelGGL(fwht_cols_kernel, dim3(grid_for((long long)b * (n / C), max_blocks)), dim3(kColThreads),
+                     (size_t)a * C * sizeof(float), stream, P2);
   return hipGetLastError();
 }
 
