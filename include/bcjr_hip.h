@@ -17,6 +17,8 @@
  *                  with the tie rules of src/viterbi/encode.py:250-307
  *   bcjr_decode    src/viterbi/encode.py:310-325 (viterbi_decode_v) and
  *                  src/qat/ste.py:270-283 (_replay_walks)
+ *   bcjr_dequant   src/quantize/serialize.py:56-107 (dequant_target, before the
+ *                  inverse RHT) and src/quantize/lut_ft.py:59-79
  *   bcjr_codebook  src/codes/ref.py:33-41,76-91 (1MAD, 3INST) and
  *                  src/qat/ste.py:376-392 (make_hyb_codebook_gpu)
  *   bcjr_hadamard  fast_hadamard_transform.hadamard_transform (src/rht/transform.py:44-55)
@@ -134,6 +136,27 @@ int bcjr_viterbi(const bcjr_problem* prob, const float* seq, const float* codebo
 int bcjr_decode(const bcjr_problem* prob, const int32_t* bitstream, const uint8_t* packed,
                 const int32_t* start_state, const float* codebook_or_lut, int32_t* walk,
                 float* recon, hipStream_t stream);
+
+/* Bitstream layouts accepted by bcjr_dequant. */
+enum {
+    BCJR_BITS_U8 = 0,     /* (B, N) uint8, one step per byte (the reference's payload) */
+    BCJR_BITS_I32 = 1,    /* (B, N) int32, as bcjr_viterbi writes it                   */
+    BCJR_BITS_PACKED = 2  /* (B, ceil(N*kV/8)) uint8, kV bits per step, LSB-first      */
+};
+
+/* Dequantize an (m, n) matrix of Tx x Ty tiles straight from its bitstreams:
+ *   out[r, c] = (float)(scale * c_v(state_t)), the product in double, with
+ *   b = (c / Ty) * (m / Tx) + r / Tx,
+ *   e = (r % Tx) * Ty + c % Ty = t * V + v,
+ * the walk replayed from start_state[b] as in bcjr_decode.  Needs
+ * m % Tx == 0, n % Ty == 0, N * V == Tx * Ty and prob->B == (m/Tx) * (n/Ty).
+ * The inverse RHT (bcjr_rht with inverse = 1) then gives the weight in the
+ * original basis.  Replaces the walk replay + untiling + scaling of
+ * dequant_target (src/quantize/serialize.py:56-107) and
+ * precompute_walk_states (src/quantize/lut_ft.py:59-79). */
+int bcjr_dequant(const bcjr_problem* prob, const void* bitstream, int bits_format,
+                 const int32_t* start_state, const float* codebook_or_lut, int64_t m,
+                 int64_t n, int Tx, int Ty, double scale, float* out, hipStream_t stream);
 
 /* Materialise the (2^L, V) codebook of prob->code (1MAD, 3INST or HYB; HYB
  * reads the (2^Q, 2) LUT in codebook_or_lut).  Bit-identical to the

@@ -23,6 +23,9 @@ Contents
                           2-bit (k*V-bit) LSB-first packing of per-step indices.
 ``fwht / rht / inverse_rht``
                           the random Hadamard transform of src/rht/transform.py.
+``walk_states / dequant_unit / dequant_target``
+                          walk replay and dequantization of saved targets
+                          (src/quantize/lut_ft.py:59-79, src/quantize/serialize.py:56-107).
 
 How each restatement is pinned (tests/test_oracle.py)
 -----------------------------------------------------
@@ -39,6 +42,11 @@ pack_bits / unpack_bits        round trips and hand-checked byte layouts.
 fwht / rht / inverse_rht       scipy.linalg.hadamard (Sylvester) matrix products,
                                bit-exact on integer inputs; rht . inverse_rht = I;
                                norm preservation.
+walk_states / dequant_*        the C decode restatement (itself pinned above); the
+                               sliding-window closed form of a state; tiles laid out
+                               independently (matrix slices) reproduce a matrix
+                               built from known walks; the scale's rounding against
+                               exact rationals.
 No function is parity unpinned.  What no check here can pin is the reference's
 own float32 rounding of its eager torch ops (no fixtures of it exist).
 """
@@ -372,3 +380,41 @@ def inverse_rht(W_tilde, sign_l, sign_r):
     Wr = fwht(W) * np.asarray(sign_r, np.float32)[None, :]
     Wl = fwht(Wr.T).T * np.asarray(sign_l, np.float32)[:, None]
     return _rht_scale(Wl, m, n)
+
+
+# ---------------------------------------------------------------------------
+# Dequantization of saved targets (src/quantize/serialize.py, lut_ft.py)
+# ---------------------------------------------------------------------------
+def walk_states(bitstreams, start_states, L, KV):
+    """State walks s_t = ((s_{t-1} << KV) | b_t) & (2^L - 1) from s_{-1} = start,
+    over any leading batch shape (src/quantize/lut_ft.py:59-79), int64."""
+    bs = np.asarray(bitstreams, dtype=np.int64)
+    s = np.asarray(start_states, dtype=np.int64).copy()
+    mask = (1 << L) - 1
+    walks = np.zeros_like(bs)
+    for t in range(bs.shape[-1]):
+        s = ((s << KV) | bs[..., t]) & mask
+        walks[..., t] = s
+    return walks
+
+
+def dequant_unit(bitstreams, start_states, cb, shape, L, KV, Tx, Ty):
+    """Unit-scale rotated-basis matrix (m, n) float64 of saved bitstreams
+    (n_col_blocks, n_row_blocks, n_steps): column block j, row block i holds
+    cb[walk] of tile (j, i) row-major (src/quantize/serialize.py:85-103)."""
+    m, n = shape
+    cb = np.asarray(cb, dtype=np.float32)
+    walks = walk_states(bitstreams, start_states, L, KV)
+    nc, nr, _ = walks.shape
+    W = np.zeros((m, n), dtype=np.float64)
+    for j in range(nc):
+        W[:, j * Ty:(j + 1) * Ty] = cb[walks[j]].reshape(nr, Tx * Ty).astype(np.float64).reshape(m, Ty)
+    return W
+
+
+def dequant_target(bitstreams, start_states, cb, sign_l, sign_r, W_scale, shape, L, KV, Tx, Ty):
+    """Weight in the original basis (src/quantize/serialize.py:56-107): the
+    float64 product W_unit * W_scale, cast to float32 by the inverse RHT
+    (src/rht/transform.py:99-126)."""
+    W_tilde = dequant_unit(bitstreams, start_states, cb, shape, L, KV, Tx, Ty) * float(W_scale)
+    return inverse_rht(W_tilde.astype(np.float32), np.asarray(sign_l, np.float32), np.asarray(sign_r, np.float32))

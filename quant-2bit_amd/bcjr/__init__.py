@@ -19,6 +19,10 @@ from .ste import (  # noqa: F401
     TrellisQuantSTE, TrellisQuantSTE_IP, ptq_residual, quantize_forward_gpu, quantize_forward_gpu_no_rht,
     replay_walks,
 )
+from .serialize import (  # noqa: F401
+    dequant_target, dequant_target_gpu, load_packed, load_quantized, pack_bitstreams, precompute_walk_states,
+    save_packed, save_quantized, unpack_bitstreams,
+)
 from ._lib import LIB_PATH, load as load_library  # noqa: F401
 
 __version__ = "0.1.0"

@@ -202,6 +202,58 @@ def decode(spec: Spec, start: torch.Tensor, table, bitstream=None, packed=None, 
         return walk, recon
 
 
+def decode_walks(spec: Spec, start: torch.Tensor, bitstream: torch.Tensor) -> torch.Tensor:
+    """Walks only: (B, N) int32 states replayed from start (B,) and a (B, N)
+    bitstream; needs no codebook."""
+    dev = start.device
+    with torch.cuda.device(dev):
+        start = start.to(torch.int32).contiguous()
+        bitstream = bitstream.to(torch.int32).contiguous()
+        B, N = bitstream.shape
+        walk = torch.empty((B, N), dtype=torch.int32, device=dev)
+        if B == 0 or N == 0:
+            return walk
+        prob = spec.problem(B, N)
+        _lib.check(_lib.load().bcjr_decode(
+            ctypes.byref(prob), _lib.ptr(bitstream), None, _lib.ptr(start), None, _lib.ptr(walk), None,
+            _stream(dev)), "bcjr_decode")
+        return walk
+
+
+BITS_U8, BITS_I32, BITS_PACKED = 0, 1, 2
+
+
+def dequant(spec: Spec, start: torch.Tensor, table, m: int, n: int, Tx: int, Ty: int, scale: float,
+            bitstream=None, packed=None) -> torch.Tensor:
+    """(m, n) float32 matrix scale * c(walk) of Tx x Ty tiles, tile b = col_block *
+    (m // Tx) + row_block, from a (B, N) uint8 / int32 bitstream or a packed one."""
+    dev = start.device
+    with torch.cuda.device(dev):
+        start = start.reshape(-1).to(torch.int32).contiguous()
+        B = start.shape[0]
+        N = (Tx * Ty) // spec.V
+        if bitstream is not None:
+            if bitstream.numel() != B * N:
+                raise AssertionError(f"bitstream has {bitstream.numel()} steps, expected {B} tiles x {N}")
+            fmt = BITS_U8 if bitstream.dtype == torch.uint8 else BITS_I32
+            bits = bitstream.reshape(B, N)
+            bits = bits.contiguous() if fmt == BITS_U8 else bits.to(torch.int32).contiguous()
+        elif packed is not None:
+            fmt = BITS_PACKED
+            nbytes = (N * spec.kV + 7) // 8
+            if packed.numel() != B * nbytes:
+                raise AssertionError(f"packed bitstream has {packed.numel()} bytes, expected {B} tiles x {nbytes}")
+            bits = packed.reshape(B, nbytes).to(torch.uint8).contiguous()
+        else:
+            raise AssertionError("need bitstream or packed")
+        out = torch.empty((m, n), dtype=torch.float32, device=dev)
+        prob = spec.problem(B, N)
+        _lib.check(_lib.load().bcjr_dequant(
+            ctypes.byref(prob), _lib.ptr(bits), fmt, _lib.ptr(start), _lib.ptr(table), m, n, Tx, Ty,
+            float(scale), _lib.ptr(out), _stream(dev)), "bcjr_dequant")
+        return out
+
+
 def codebook(code: int, L: int, device, lut: torch.Tensor | None = None, Q: int = 9) -> torch.Tensor:
     """(2^L, V) float32 codebook from a generator (1MAD, 3INST or HYB)."""
     device = torch.device(device)
@@ -215,5 +267,5 @@ def codebook(code: int, L: int, device, lut: torch.Tensor | None = None, Q: int 
     return out
 
 
-__all__ = ["Spec", "forward", "forward_internals", "backward", "viterbi", "decode", "codebook",
-           "CODE_TABLE", "CODE_1MAD", "CODE_3INST", "CODE_HYB"]
+__all__ = ["Spec", "forward", "forward_internals", "backward", "viterbi", "decode", "decode_walks", "dequant",
+           "codebook", "CODE_TABLE", "CODE_1MAD", "CODE_3INST", "CODE_HYB"]

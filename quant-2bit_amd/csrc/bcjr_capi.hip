@@ -451,6 +451,43 @@ int bcjr_decode(const bcjr_problem* prob, const int32_t* bitstream, const uint8_
   return BCJR_OK;
 }
 
+int bcjr_dequant(const bcjr_problem* prob, const void* bitstream, int bits_format,
+                 const int32_t* start_state, const float* codebook_or_lut, int64_t m, int64_t n, int Tx,
+                 int Ty, double scale, float* out, hipStream_t stream) {
+  int rc = validate(prob);
+  if (rc) return rc;
+  if (Tx < 1 || Ty < 1) return fail(BCJR_EINVAL, "tile %dx%d must be positive", Tx, Ty);
+  if (m < 0 || n < 0 || m % Tx || n % Ty)
+    return fail(BCJR_EINVAL, "matrix %lldx%lld is not a whole number of %dx%d tiles", (long long)m,
+                (long long)n, Tx, Ty);
+  if ((long long)Tx * Ty != prob->N * prob->V)
+    return fail(BCJR_EINVAL, "tile %dx%d holds %lld weights, sequences N*V=%lld", Tx, Ty,
+                (long long)Tx * Ty, (long long)(prob->N * prob->V));
+  if (prob->B != (m / Tx) * (n / Ty))
+    return fail(BCJR_EINVAL, "B=%lld but the matrix has %lld tiles", (long long)prob->B,
+                (long long)((m / Tx) * (n / Ty)));
+  if (bits_format != BCJR_BITS_U8 && bits_format != BCJR_BITS_I32 && bits_format != BCJR_BITS_PACKED)
+    return fail(BCJR_EINVAL, "unknown bitstream format %d", bits_format);
+  if (prob->B == 0) return BCJR_OK;
+  if (!bitstream || !start_state || !out) return fail(BCJR_EINVAL, "bitstream, start_state and out are required");
+  if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
+    return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  const int KV = prob->k * prob->V;
+  const void* fn = bcjr::dequant_kernel_ptr(KV, prob->V, prob->code);
+  if (!fn) return fail(BCJR_EUNSUPPORTED, "no dequant kernel for k*V=%d V=%d code=%d", KV, prob->V, prob->code);
+  bcjr::DqParams P = {bits_format == BCJR_BITS_I32 ? static_cast<const int32_t*>(bitstream) : nullptr,
+                      bits_format == BCJR_BITS_U8 ? static_cast<const uint8_t*>(bitstream) : nullptr,
+                      bits_format == BCJR_BITS_PACKED ? static_cast<const uint8_t*>(bitstream) : nullptr,
+                      start_state, codebook_or_lut, out, m, n, (int)prob->N, prob->L, prob->Q, Tx, Ty,
+                      scale};
+  void* args[] = {&P};
+  const long long blocks = (m * n + 255) / 256;
+  const unsigned grid = (unsigned)(blocks < 16384 ? blocks : 16384);
+  hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, stream);
+  if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel(dequant)");
+  return BCJR_OK;
+}
+
 int bcjr_codebook(const bcjr_problem* prob, const float* lut, float* codebook_out, hipStream_t stream) {
   if (!prob) return fail(BCJR_EINVAL, "problem is NULL");
   if (prob->L < 1 || prob->L > 24) return fail(BCJR_EINVAL, "L=%d outside [1, 24]", prob->L);

@@ -346,6 +346,18 @@ struct DecParams {
   int N, L, Q;
 };
 
+struct DqParams {
+  const int32_t* bits32;  // (B, N) one step per int32, or null
+  const uint8_t* bits8;   // (B, N) one step per byte (the reference's payload), or null
+  const uint8_t* packed;  // (B, ceil(N*kV/8)) kV bits per step, LSB-first, or null
+  const int32_t* start;   // (B,)
+  const float* table;     // codebook or HYB LUT (global)
+  float* out;             // (m, n) row-major
+  long long m, n;
+  int N, L, Q, Tx, Ty;
+  double scale;           // the product is rounded once to float32, as numpy does
+};
+
 struct CbParams {
   const float* lut;  // HYB LUT or null
   float* out;        // (S, V)

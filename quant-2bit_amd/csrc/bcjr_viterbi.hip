@@ -288,6 +288,51 @@ __global__ __launch_bounds__(256) void bcjr_decode_kernel(DecParams P) {
   }
 }
 
+// Dequantize tiles straight into the matrix: out[row, col] = fl32(scale * c_v(s_t))
+// (product in double, one rounding: the float64 product then float32 cast of
+// src/quantize/serialize.py:106 and src/rht/transform.py:110)
+// with the tile order of tile_for_viterbi (sequence b = col_block * n_row_blocks
+// + row_block holds the Tx x Ty tile row-major, element e = t*V + v).  The walk
+// state needs no serial replay: s_t = ((start << kV(t+1)) | sum_{tau<=t}
+// bits_tau << kV(t - tau)) mod 2^L depends only on the last ceil(L/kV) steps (and
+// on start while kV(t+1) < L), so every output element is decoded by its own thread
+// and the writes are coalesced along rows.
+template <int KV, int V, int CODE>
+__global__ __launch_bounds__(256) void bcjr_dequant_kernel(DqParams P) {
+  constexpr int R = 1 << KV;
+  const uint32_t mask = (P.L >= 32) ? 0xFFFFFFFFu : ((1u << P.L) - 1u);
+  const int steps = (P.L + KV - 1) / KV;  // steps whose bits reach a state
+  const int nbytes = (P.N * KV + 7) / 8;
+  const long long n_row = P.m / P.Tx;
+  const long long total = P.m * P.n;
+  for (long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (long long)gridDim.x * blockDim.x) {
+    const long long row = idx / P.n, col = idx - row * P.n;
+    const long long b = (col / P.Ty) * n_row + row / P.Tx;
+    const int e = (int)((row % P.Tx) * P.Ty + col % P.Ty);
+    const int t = e / V, v = e - (e / V) * V;
+    uint32_t s = 0;
+    if (KV * (t + 1) < P.L) s = ((uint32_t)P.start[b] << (KV * (t + 1))) & mask;
+    const int lo = t - steps + 1 > 0 ? t - steps + 1 : 0;
+    for (int tau = lo; tau <= t; ++tau) {
+      uint32_t bits;
+      if (P.packed) {
+        constexpr int per = 8 / KV;
+        bits = ((uint32_t)P.packed[(size_t)b * nbytes + tau / per] >> ((tau % per) * KV)) & (R - 1);
+      } else if (P.bits8) {
+        bits = (uint32_t)P.bits8[(size_t)b * P.N + tau] & (R - 1);
+      } else {
+        bits = (uint32_t)P.bits32[(size_t)b * P.N + tau] & (R - 1);
+      }
+      s |= bits << (KV * (t - tau));
+    }
+    s &= mask;
+    float c[V];
+    codeword<CODE, V>(s, P.table, P.table, P.Q, c);
+    P.out[idx] = (float)((double)c[v] * P.scale);
+  }
+}
+
 // Codebook fill: one thread per state.
 template <int CODE>
 __global__ __launch_bounds__(256) void bcjr_codebook_kernel(CbParams P) {
@@ -342,6 +387,25 @@ const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache) {
 #define BCJR_DEC_CASE(KV_, V_, CODE_) \
   if (KV == KV_ && V == V_ && code == CODE_) \
     return reinterpret_cast<const void*>(&bcjr_decode_kernel<KV_, V_, CODE_>);
+
+#define BCJR_DQ_CASE(KV_, V_, CODE_) \
+  if (KV == KV_ && V == V_ && code == CODE_) \
+    return reinterpret_cast<const void*>(&bcjr_dequant_kernel<KV_, V_, CODE_>);
+
+const void* dequant_kernel_ptr(int KV, int V, int code) {
+  BCJR_DQ_CASE(1, 1, CODE_TABLE)
+  BCJR_DQ_CASE(2, 1, CODE_TABLE)
+  BCJR_DQ_CASE(2, 1, CODE_1MAD)
+  BCJR_DQ_CASE(2, 1, CODE_3INST)
+  BCJR_DQ_CASE(2, 2, CODE_TABLE)
+  BCJR_DQ_CASE(2, 2, CODE_HYB)
+  BCJR_DQ_CASE(4, 1, CODE_TABLE)
+  BCJR_DQ_CASE(4, 1, CODE_1MAD)
+  BCJR_DQ_CASE(4, 1, CODE_3INST)
+  BCJR_DQ_CASE(4, 2, CODE_TABLE)
+  BCJR_DQ_CASE(4, 2, CODE_HYB)
+  return nullptr;
+}
 
 const void* decode_kernel_ptr(int KV, int V, int code) {
   BCJR_DEC_CASE(1, 1, CODE_TABLE)
