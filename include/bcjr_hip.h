@@ -24,6 +24,8 @@
  *   bcjr_hadamard  fast_hadamard_transform.hadamard_transform (src/rht/transform.py:44-55)
  *   bcjr_rht       src/qat/ste.py:113-135 (apply_rht_gpu, apply_inverse_rht_gpu),
  *                  src/rht/transform.py:65-126
+ *   bcjr_rht_batched  the per-expert RHT calls of src/qat/qat_moe_layer.py:106-114,
+ *                  in one launch pair
  *
  * Conventions
  *   - All pointers are device pointers owned by the caller; inputs are read-only.
@@ -182,6 +184,15 @@ int bcjr_hadamard(const float* x, float* out, int64_t rows, int64_t n, float sca
  * (src/rht/transform.py:65-126). */
 int bcjr_rht(const float* W, float* out, int64_t m, int64_t n, const float* sign_l,
              const float* sign_r, int inverse, hipStream_t stream);
+
+/* bcjr_rht over a batch of (m, n) matrices W (batch, m, n) with one pair of
+ * sign vectors per matrix, sign_l (batch, m) and sign_r (batch, n); matrix e of
+ * out is bcjr_rht of matrix e of W, in two launches for the whole batch.  No
+ * single reference function: it serves the expert-batched dispatch that
+ * replaces the per-expert loop of src/qat/qat_moe_layer.py:106-114 (each
+ * expert's QuantizedLinear calling apply_rht_gpu, src/qat/ste.py:113-135). */
+int bcjr_rht_batched(const float* W, float* out, int64_t batch, int64_t m, int64_t n,
+                     const float* sign_l, const float* sign_r, int inverse, hipStream_t stream);
 
 /* Static name of a status code. */
 const char* bcjr_strerror(int status);

@@ -14,7 +14,11 @@ from .viterbi import (  # noqa: F401
 from .quant import (  # noqa: F401
     bcjr_quantize_tiles, bcjr_quantize_weight, bcjr_quantize_weight_rotated, tile_for_viterbi, untile_from_viterbi,
 )
-from .rht import apply_inverse_rht_gpu, apply_rht_gpu, hadamard_transform, make_sign_vector  # noqa: F401
+from .rht import (  # noqa: F401
+    apply_inverse_rht_batched, apply_inverse_rht_gpu, apply_rht_batched, apply_rht_gpu, hadamard_transform,
+    make_sign_vector,
+)
+from .experts import bcjr_quantize_experts, quantize_moe_experts  # noqa: F401
 from .ste import (  # noqa: F401
     TrellisQuantSTE, TrellisQuantSTE_IP, ptq_residual, quantize_forward_gpu, quantize_forward_gpu_no_rht,
     replay_walks,

@@ -5,7 +5,10 @@ Drop-in for the GPU RHT of the reference:
     used by src/rht/transform.py:44-55 and src/qat/ste.py:113-135;
   * apply_rht_gpu / apply_inverse_rht_gpu (src/qat/ste.py:113-135), which equal
     apply_rht / apply_inverse_rht of src/rht/transform.py:65-126;
-  * make_sign_vector (src/rht/transform.py:58-62).
+  * make_sign_vector (src/rht/transform.py:58-62);
+  * apply_rht_batched / apply_inverse_rht_batched: the same transforms on a
+    batch (E, m, n) with per-matrix sign vectors, in one launch pair (used by
+    the expert-batched dispatch).
 
 RHT(W) = H_m diag(sl) W diag(sr) H_n / sqrt(m n) is linear and its adjoint is
 the inverse transform, so the autograd backward of each is the other one.
@@ -95,6 +98,46 @@ class RhtFunction(torch.autograd.Function):
         return _rht(g.contiguous(), sign_l, sign_r, not ctx.inverse), None, None, None
 
 
+def _rht_batched(W, sign_l, sign_r, inverse: bool) -> torch.Tensor:
+    if W.dim() != 3 or not W.is_cuda or W.dtype != torch.float32:
+        raise AssertionError(f"W must be a 3-D float32 GPU tensor; got {tuple(W.shape)} {W.dtype}")
+    E, m, n = W.shape
+    if tuple(sign_l.shape) != (E, m) or tuple(sign_r.shape) != (E, n):
+        raise AssertionError(f"sign vectors must be ({E}, {m}) and ({E}, {n}); got {tuple(sign_l.shape)}, "
+                             f"{tuple(sign_r.shape)}")
+    Wc = W.detach().contiguous()
+    sl = sign_l.detach().to(device=W.device, dtype=torch.float32).contiguous()
+    sr = sign_r.detach().to(device=W.device, dtype=torch.float32).contiguous()
+    out = torch.empty_like(Wc)
+    with torch.cuda.device(W.device):
+        _lib.check(_lib.load().bcjr_rht_batched(_lib.ptr(Wc), _lib.ptr(out), E, m, n, _lib.ptr(sl), _lib.ptr(sr),
+                                                1 if inverse else 0, _stream(W.device)), "bcjr_rht_batched")
+    return out
+
+
+class RhtBatchedFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, W, sign_l, sign_r, inverse):
+        ctx.save_for_backward(sign_l, sign_r)
+        ctx.inverse = inverse
+        return _rht_batched(W, sign_l, sign_r, inverse)
+
+    @staticmethod
+    def backward(ctx, g):
+        sign_l, sign_r = ctx.saved_tensors
+        return _rht_batched(g.contiguous(), sign_l, sign_r, not ctx.inverse), None, None, None
+
+
+def apply_rht_batched(W, sign_l, sign_r):
+    """apply_rht_gpu on each matrix of W (E, m, n), signs (E, m) and (E, n)."""
+    return RhtBatchedFunction.apply(W, sign_l, sign_r, False)
+
+
+def apply_inverse_rht_batched(W_tilde, sign_l, sign_r):
+    """apply_inverse_rht_gpu on each matrix of W_tilde (E, m, n)."""
+    return RhtBatchedFunction.apply(W_tilde, sign_l, sign_r, True)
+
+
 def apply_rht_gpu(W, sign_l_gpu, sign_r_gpu):
     """W~ = H_m diag(sl) W diag(sr) H_n / sqrt(m n)  (src/qat/ste.py:113-126)."""
     return RhtFunction.apply(W, sign_l_gpu, sign_r_gpu, False)
@@ -105,4 +148,5 @@ def apply_inverse_rht_gpu(W_tilde, sign_l_gpu, sign_r_gpu):
     return RhtFunction.apply(W_tilde, sign_l_gpu, sign_r_gpu, True)
 
 
-__all__ = ["make_sign_vector", "hadamard_transform", "apply_rht_gpu", "apply_inverse_rht_gpu"]
+__all__ = ["make_sign_vector", "hadamard_transform", "apply_rht_gpu", "apply_inverse_rht_gpu", "apply_rht_batched",
+           "apply_inverse_rht_batched"]

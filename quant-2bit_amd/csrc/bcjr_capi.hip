@@ -306,6 +306,38 @@ int launch(const Plan& pl, long long B, size_t ws_bytes, void* params, hipStream
 
 }  // namespace
 
+namespace {
+
+int rht_impl(const float* W, float* out, int64_t batch, int64_t m, int64_t n, const float* sign_l,
+             const float* sign_r, int inverse, hipStream_t stream) {
+  if (batch < 0 || batch > INT32_MAX) return fail(BCJR_EINVAL, "batch=%lld outside [0, 2^31)", (long long)batch);
+  if (m < 1 || m > 16384 || (m & (m - 1)))
+    return fail(BCJR_EINVAL, "m=%lld must be a power of two in [1, 16384]", (long long)m);
+  if (n < 1 || n > 16384 || (n & (n - 1)))
+    return fail(BCJR_EINVAL, "n=%lld must be a power of two in [1, 16384]", (long long)n);
+  if (batch == 0) return BCJR_OK;
+  if (!W || !out || !sign_l || !sign_r) return fail(BCJR_EINVAL, "W, out, sign_l and sign_r must be non-NULL");
+  const size_t bytes = (size_t)batch * m * n * sizeof(float);
+  const char *w0 = reinterpret_cast<const char*>(W), *o0 = reinterpret_cast<const char*>(out);
+  if (w0 < o0 + bytes && o0 < w0 + bytes) return fail(BCJR_EINVAL, "out must not alias W");
+  DeviceInfo di;
+  int rc = device_info(&di);
+  if (rc) return rc;
+  const float s = (float)(1.0 / sqrt((double)m * (double)n));
+  const int blocks = di.num_cu * 8;
+  const long long rows = batch * m;
+  // forward: rows of W diag(sr) H_n, then row signs, then H_m and the scale;
+  // inverse: rows of W H_n then diag(sr), then H_m, row signs and the scale.
+  hipError_t e =
+      inverse ? bcjr::launch_fwht_rows(W, out, rows, (int)n, nullptr, sign_r, m, nullptr, 1.0f, blocks, stream)
+              : bcjr::launch_fwht_rows(W, out, rows, (int)n, sign_r, nullptr, m, sign_l, 1.0f, blocks, stream);
+  if (e != hipSuccess) return hip_fail(e, "bcjr_rht row pass");
+  e = bcjr::launch_fwht_cols(out, (int)batch, (int)m, (int)n, inverse ? sign_l : nullptr, s, blocks, stream);
+  return e == hipSuccess ? BCJR_OK : hip_fail(e, "bcjr_rht column pass");
+}
+
+}  // namespace
+
 extern "C" {
 
 int bcjr_workspace_bytes(const bcjr_problem* prob, int op, size_t* bytes) {
@@ -513,31 +545,20 @@ int bcjr_hadamard(const float* x, float* out, int64_t rows, int64_t n, float sca
   DeviceInfo di;
   int rc = device_info(&di);
   if (rc) return rc;
-  hipError_t e = bcjr::launch_fwht_rows(x, out, rows, (int)n, nullptr, nullptr, nullptr, scale, di.num_cu * 8,
+  hipError_t e = bcjr::launch_fwht_rows(x, out, rows, (int)n, nullptr, nullptr, rows, nullptr, scale, di.num_cu * 8,
                                         stream);
   return e == hipSuccess ? BCJR_OK : hip_fail(e, "bcjr_hadamard launch");
 }
 
+
 int bcjr_rht(const float* W, float* out, int64_t m, int64_t n, const float* sign_l, const float* sign_r,
              int inverse, hipStream_t stream) {
-  if (m < 1 || m > 16384 || (m & (m - 1)))
-    return fail(BCJR_EINVAL, "m=%lld must be a power of two in [1, 16384]", (long long)m);
-  if (n < 1 || n > 16384 || (n & (n - 1)))
-    return fail(BCJR_EINVAL, "n=%lld must be a power of two in [1, 16384]", (long long)n);
-  if (!W || !out || !sign_l || !sign_r) return fail(BCJR_EINVAL, "W, out, sign_l and sign_r must be non-NULL");
-  if (W == out) return fail(BCJR_EINVAL, "out must not alias W");
-  DeviceInfo di;
-  int rc = device_info(&di);
-  if (rc) return rc;
-  const float s = (float)(1.0 / sqrt((double)m * (double)n));
-  const int blocks = di.num_cu * 8;
-  // forward: rows of W diag(sr) H_n, then row signs, then H_m and the scale;
-  // inverse: rows of W H_n then diag(sr), then H_m, row signs and the scale.
-  hipError_t e = inverse ? bcjr::launch_fwht_rows(W, out, m, (int)n, nullptr, sign_r, nullptr, 1.0f, blocks, stream)
-                         : bcjr::launch_fwht_rows(W, out, m, (int)n, sign_r, nullptr, sign_l, 1.0f, blocks, stream);
-  if (e != hipSuccess) return hip_fail(e, "bcjr_rht row pass");
-  e = bcjr::launch_fwht_cols(out, (int)m, (int)n, inverse ? sign_l : nullptr, s, blocks, stream);
-  return e == hipSuccess ? BCJR_OK : hip_fail(e, "bcjr_rht column pass");
+  return rht_impl(W, out, 1, m, n, sign_l, sign_r, inverse, stream);
+}
+
+int bcjr_rht_batched(const float* W, float* out, int64_t batch, int64_t m, int64_t n, const float* sign_l,
+                     const float* sign_r, int inverse, hipStream_t stream) {
+  return rht_impl(W, out, batch, m, n, sign_l, sign_r, inverse, stream);
 }
 
 const char* bcjr_strerror(int status) {

@@ -42,10 +42,10 @@ const void* codebook_kernel_ptr(int code);
 // post .* H_n (pre .* x[r]), n a power of two <= 16384, out may equal x.
 // Columns: x = scale * diag(row_sign) H_m x in place, m, n <= 16384 powers of two.
 hipError_t launch_fwht_rows(const float* x, float* out, long long rows, int n, const float* pre,
-                            const float* post, const float* row_sign, float scale, int max_blocks,
-                            hipStream_t stream);
-hipError_t launch_fwht_cols(float* x, int m, int n, const float* row_sign, float scale, int max_blocks,
-                            hipStream_t stream);
+                            const float* post, long long vec_rows, const float* row_sign, float scale,
+                            int max_blocks, hipStream_t stream);
+hipError_t launch_fwht_cols(float* x, int batch, int m, int n, const float* row_sign, float scale,
+                            int max_blocks, hipStream_t stream);
 
 // LDS bytes for one workgroup.
 inline size_t fwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {

@@ -8,6 +8,9 @@
 // float32 additions is the reference's and the results agree bit for bit (the
 // final scale is a multiply by s, exact whenever m*n is an even power of two).
 //
+// A batch of matrices (E, m, n) with per-matrix sign vectors (E, m), (E, n) runs
+// in the same launches (expert-batched dispatch).
+//
 // Rows (last axis, contiguous): one workgroup per row, staged in LDS (n <= 16384).
 // Columns (first axis, stride n): m = a*b with b = min(m, 128); a first pass does
 // the stages h < b on tiles of b consecutive rows x 64 consecutive columns, a
@@ -44,8 +47,9 @@ struct RowsParams {
   float* out;
   long long rows;
   int n;
-  const float* pre;       // (n) multiplies x before the transform, or null
-  const float* post;      // (n) multiplies the result, or null
+  const float* pre;       // (rows / vec_rows, n) multiplies x before the transform, or null
+  const float* post;      // (rows / vec_rows, n) multiplies the result, or null
+  long long vec_rows;     // consecutive rows sharing one pre/post vector (m of a batch)
   const float* row_sign;  // (rows) multiplies row r of the result, or null
   float scale;
 };
@@ -55,7 +59,8 @@ __global__ __launch_bounds__(kRowThreads) void fwht_rows_kernel(RowsParams P) {
   const int n = P.n, tid = threadIdx.x, nthr = blockDim.x;
   for (long long r = blockIdx.x; r < P.rows; r += gridDim.x) {
     const float* xr = P.x + (size_t)r * n;
-    for (int i = tid; i < n; i += nthr) v[i] = P.pre ? xr[i] * P.pre[i] : xr[i];
+    const size_t vo = (size_t)(r / P.vec_rows) * n;
+    for (int i = tid; i < n; i += nthr) v[i] = P.pre ? xr[i] * P.pre[vo + i] : xr[i];
     __syncthreads();
     for (int h = 1; h < n; h <<= 1) {
       stage(v, n, h, tid, nthr);
@@ -65,7 +70,7 @@ __global__ __launch_bounds__(kRowThreads) void fwht_rows_kernel(RowsParams P) {
     float* orow = P.out + (size_t)r * n;
     for (int i = tid; i < n; i += nthr) {
       float y = v[i];
-      if (P.post) y *= P.post[i];
+      if (P.post) y *= P.post[vo + i];
       orow[i] = (y * rs) * P.scale;
     }
     __syncthreads();
@@ -73,14 +78,17 @@ __global__ __launch_bounds__(kRowThreads) void fwht_rows_kernel(RowsParams P) {
 }
 
 struct ColsParams {
-  float* x;               // (m, n) transformed in place
+  float* x;               // (batch, m, n) transformed in place
+  long long mat_stride;   // m * n
+  int m;                  // rows per matrix (row_sign offset of matrix e is e * m)
   int n;
   int C;                  // tile width: min(kColTile, n), a power of two dividing n
   int len;                // transform length along the column (tile rows)
   long long step;         // floats between consecutive tile rows
   long long outer_stride; // floats between tiles of consecutive outer index
   int outer;              // outer index count
-  const float* row_sign;  // (m) multiplies row o*row_o + p*row_p of the result, or null
+  int batch;              // matrices
+  const float* row_sign;  // (batch, m) multiplies row o*row_o + p*row_p of the result, or null
   int row_o, row_p;
   float scale;
 };
@@ -90,10 +98,13 @@ __global__ __launch_bounds__(kColThreads) void fwht_cols_kernel(ColsParams P) {
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int C = P.C;
   const int ncb = P.n / C;
-  const long long tiles = (long long)P.outer * ncb;
+  const long long per_mat = (long long)P.outer * ncb;
+  const long long tiles = per_mat * P.batch;
   for (long long g = blockIdx.x; g < tiles; g += gridDim.x) {
-    const int o = (int)(g / ncb), cb = (int)(g % ncb);
-    float* base = P.x + (size_t)o * P.outer_stride + (size_t)cb * C;
+    const long long e = g / per_mat, gm = g - e * per_mat;
+    const int o = (int)(gm / ncb), cb = (int)(gm % ncb);
+    float* base = P.x + (size_t)e * P.mat_stride + (size_t)o * P.outer_stride + (size_t)cb * C;
+    const float* rsgn = P.row_sign ? P.row_sign + (size_t)e * P.m : nullptr;
     for (int e = tid; e < P.len * C; e += nthr) {
       const int p = e / C, c = e % C;
       t[e] = base[(size_t)p * P.step + c];
@@ -114,7 +125,7 @@ __global__ __launch_bounds__(kColThreads) void fwht_cols_kernel(ColsParams P) {
     for (int e = tid; e < P.len * C; e += nthr) {
       const int p = e / C, c = e % C;
       float y = t[e];
-      if (P.row_sign) y *= P.row_sign[o * P.row_o + p * P.row_p];
+      if (rsgn) y *= rsgn[o * P.row_o + p * P.row_p];
       base[(size_t)p * P.step + c] = y * P.scale;
     }
     __syncthreads();
@@ -129,38 +140,41 @@ int grid_for(long long items, int max_blocks) {
 
 // Host launchers used by the C ABI.  Shapes are validated by the caller.
 hipError_t launch_fwht_rows(const float* x, float* out, long long rows, int n, const float* pre,
-                            const float* post, const float* row_sign, float scale, int max_blocks,
-                            hipStream_t stream) {
+                            const float* post, long long vec_rows, const float* row_sign, float scale,
+                            int max_blocks, hipStream_t stream) {
   if (rows == 0) return hipSuccess;
-  RowsParams P = {x, out, rows, n, pre, post, row_sign, scale};
+  RowsParams P = {x, out, rows, n, pre, post, vec_rows > 0 ? vec_rows : rows, row_sign, scale};
   const size_t lds = (size_t)n * sizeof(float);  // n <= 16384: at most 64 KiB
   hipLaunchKernelGGL(fwht_rows_kernel, dim3(grid_for(rows, max_blocks)), dim3(kRowThreads), lds, stream, P);
   return hipGetLastError();
 }
 
-// H_m applied to every column of the (m, n) matrix x, in place; the result is
-// multiplied by row_sign (after the transform) and scale.  m, n powers of two.
-hipError_t launch_fwht_cols(float* x, int m, int n, const float* row_sign, float scale, int max_blocks,
-                            hipStream_t stream) {
+// H_m applied to every column of each (m, n) matrix of x (batch of them), in
+// place; the result is multiplied by row_sign (batch, m) (after the transform)
+// and scale.  m, n powers of two.
+hipError_t launch_fwht_cols(float* x, int batch, int m, int n, const float* row_sign, float scale,
+                            int max_blocks, hipStream_t stream) {
+  if (batch == 0) return hipSuccess;
+  const long long ms = (long long)m * n;
   const int b = m < 128 ? m : 128;
   const int a = m / b;
   const int C = n < kColTile ? n : kColTile;
   // pass 1: stages h < b, tiles of b consecutive rows
-  ColsParams P1 = {x, n, C, b, n, (long long)b * n, a, nullptr, 0, 0, 1.0f};
+  ColsParams P1 = {x, ms, m, n, C, b, n, (long long)b * n, a, batch, nullptr, 0, 0, 1.0f};
   if (a == 1) {  // the only pass: signs and scale here
     P1.row_sign = row_sign;
     P1.row_o = 0;
     P1.row_p = 1;
     P1.scale = scale;
   }
-  hipLaunchKernelGGL(fwht_cols_kernel, dim3(grid_for((long long)a * (n / C), max_blocks)), dim3(kColThreads),
-                     (size_t)b * C * sizeof(float), stream, P1);
+  hipLaunchKernelGGL(fwht_cols_kernel, dim3(grid_for((long long)batch * a * (n / C), max_blocks)),
+                     dim3(kColThreads), (size_t)b * C * sizeof(float), stream, P1);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a == 1) return e;
   // pass 2: stages h >= b, tiles of a rows spaced b apart (row = ia*b + ib)
-  ColsParams P2 = {x, n, C, a, (long long)b * n, n, b, row_sign, 1, b, scale};
-  hipLaunchKernelGGL(fwht_cols_kernel, dim3(grid_for((long long)b * (n / C), max_blocks)), dim3(kColThreads),
-                     (size_t)a * C * sizeof(float), stream, P2);
+  ColsParams P2 = {x, ms, m, n, C, a, (long long)b * n, n, b, batch, row_sign, 1, b, scale};
+  hipLaunchKernelGGL(fwht_cols_kernel, dim3(grid_for((long long)batch * b * (n / C), max_blocks)),
+                     dim3(kColThreads), (size_t)a * C * sizeof(float), stream, P2);
   return hipGetLastError();
 }
 

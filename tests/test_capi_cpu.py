@@ -159,3 +159,29 @@ def test_sign_vector_generator_matches_reference_draw():
     s = bcjr.make_sign_vector(1000, 7)
     ref = np.random.default_rng(7).choice([-1.0, 1.0], size=1000).astype(np.float32)
     assert s.dtype == np.float32 and np.array_equal(s, ref)
+
+
+def test_rht_batched_validation_without_device(lib):
+    p = ctypes.c_void_p(16)
+    assert lib.bcjr_rht_batched(p, ctypes.c_void_p(1 << 20), -1, 64, 64, p, p, 0, None) == -1
+    assert "batch=-1" in lib.bcjr_last_error().decode()
+    assert lib.bcjr_rht_batched(None, None, 0, 64, 64, None, None, 0, None) == 0  # nothing to do
+    assert lib.bcjr_rht_batched(p, p, 2, 64, 48, p, p, 0, None) == -1
+    assert "n=48" in lib.bcjr_last_error().decode()
+    # out overlapping the second matrix of W
+    assert lib.bcjr_rht_batched(ctypes.c_void_p(4096), ctypes.c_void_p(4096 + 64 * 64 * 4), 2, 64, 64, p, p, 0,
+                                None) == -1
+    assert "alias" in lib.bcjr_last_error().decode()
+
+
+def test_expert_dispatch_validates_before_device():
+    import bcjr
+    W = [torch.zeros(64, 64), torch.zeros(64, 40)]
+    s = [torch.ones(64), torch.ones(64)]
+    with pytest.raises(AssertionError, match="not tileable"):
+        bcjr.bcjr_quantize_experts(W, s, [torch.ones(64), torch.ones(40)], None, 0.1)
+    with pytest.raises(AssertionError, match="sign vectors"):
+        bcjr.bcjr_quantize_experts(W, s[:1], s, None, 0.1)
+    with pytest.raises(AssertionError, match="expected 1 or 2"):
+        bcjr.bcjr_quantize_experts([torch.zeros(64, 64)] * 2, s, s, None, [0.1, 0.2, 0.3])
+    assert bcjr.bcjr_quantize_experts([], [], [], None, 0.1) == []
