@@ -19,6 +19,11 @@ Also reported:
     4,096-sequence fwd+bwd timed at each per-tensor temperature of that layer,
     plus the Viterbi pack of every tile and the random Hadamard transforms
     around each weight tensor;
+  * dequantization of one Llama-3.2-1B layer from the packed 2-bit format
+    (bcjr_dequant + inverse RHT per tensor), with the dequant kernel's HBM
+    roofline;
+  * the expert-batched dispatch on OLMoE-1B-7B expert shapes against the
+    per-weight loop, and the 64-expert layer time it implies;
   * the CPU oracle (C/OpenMP) timed on a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--config tile|cpu]
@@ -65,6 +70,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=256, help="sequences in the CPU baseline sample")
     ap.add_argument("--no-layer", action="store_true", help="skip the per-temperature layer estimate")
+    ap.add_argument("--no-dequant", action="store_true", help="skip the dequant (on-disk format) leg")
+    ap.add_argument("--experts", type=int, default=2,
+                    help="OLMoE experts in the expert-batched dispatch leg (0 skips it)")
     return ap.parse_args()
 
 
@@ -216,6 +224,12 @@ def main():
     layer = None
     if args.config == "tile" and not args.no_layer:
         layer = layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev)
+    dequant = None
+    if args.config == "tile" and not args.no_dequant:
+        dequant = dequant_estimate(torch, bcjr, ops, dev)
+    experts = None
+    if args.config == "tile" and args.experts > 0:
+        experts = experts_estimate(torch, bcjr, dev, args.experts, args.T)
     calibration_copy(torch, dev)
     cpu = None
     if not args.no_cpu_baseline:
@@ -230,6 +244,7 @@ def main():
         "layer_step_s": layer["seconds"] if layer else None,
         "layer": layer,
         "roofline": roofline, "kernels": kernels,
+        "dequant": dequant, "experts": experts,
         "peaks_per_s": {k_: v["per_s"] for k_, v in peaks.items()},
         "cpu_baseline": cpu,
     }
@@ -306,6 +321,105 @@ def layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev):
             "note": "fwd+bwd per tensor timed on a %d-sequence batch at that tensor's T, scaled by its "
                     "sequence count, plus one Viterbi pack of every tile and four random Hadamard "
                     "transforms per tensor" % B}
+
+
+def dequant_estimate(torch, bcjr, ops, dev):
+    """Dequantization of a Llama-3.2-1B decoder layer from the packed 2-bit format
+    (HYB L=16, k=2, V=2): bcjr_dequant per tensor (walk replay + codebook +
+    untiling + scale into the rotated-basis matrix) and the inverse RHT after it.
+    Algorithmic bytes of bcjr_dequant per weight: a 4-byte write plus k/8 bytes
+    of packed bitstream (2 bits); the kernel is HBM-bound."""
+    import numpy as np
+    lut = np.random.default_rng(5).standard_normal((512, 2)).astype(np.float32)
+    cb = bcjr.make_hyb_codebook_gpu(lut, 9, 16, dev)
+    spec = ops.Spec(16, 2, 2, ops.CODE_HYB, 9)
+    stream = torch.cuda.current_stream(dev)
+    per, tot_k, tot_r, tot_bytes = {}, 0.0, 0.0, 0.0
+    for name, rows, cols, _ in LAYER_TENSORS:
+        B = rows * cols // 256
+        g = torch.Generator(dev).manual_seed(rows + cols)
+        packed = torch.randint(0, 256, (B, 64), dtype=torch.uint8, device=dev, generator=g)
+        start = torch.randint(0, 1 << 16, (B,), dtype=torch.int32, device=dev, generator=g)
+        sl = torch.ones(rows, device=dev)
+        sr = torch.ones(cols, device=dev)
+        W = ops.dequant(spec, start, cb._bcjr_lut, rows, cols, 16, 16, 0.02, packed=packed)
+        bcjr.apply_inverse_rht_gpu(W, sl, sr)
+        reps = 5
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record(stream)
+        for _ in range(reps):
+            W = ops.dequant(spec, start, cb._bcjr_lut, rows, cols, 16, 16, 0.02, packed=packed)
+        e[1].record(stream)
+        for _ in range(reps):
+            Wh = bcjr.apply_inverse_rht_gpu(W, sl, sr)
+        e[2].record(stream)
+        torch.cuda.synchronize(dev)
+        kd = e[0].elapsed_time(e[1]) / 1e3 / reps
+        kr = e[1].elapsed_time(e[2]) / 1e3 / reps
+        nbytes = rows * cols * (4.0 + 2.0 / 8.0) + 4.0 * B
+        per[name] = {"dequant_us": kd * 1e6, "inverse_rht_us": kr * 1e6, "GB_s": nbytes / kd / 1e9}
+        tot_k += kd
+        tot_r += kr
+        tot_bytes += nbytes
+        del W, Wh
+    # per launch, on the largest tensor (gate: 8192 x 2048, 16.8M weights)
+    big = max(LAYER_TENSORS, key=lambda t: t[1] * t[2])
+    achieved = big[1] * big[2] * 4.25 / (per[big[0]]["dequant_us"] * 1e-6)
+    return {"layer_seconds": tot_k + tot_r, "dequant_seconds": tot_k, "inverse_rht_seconds": tot_r,
+            "layer_GB_s": tot_bytes / tot_k / 1e9,
+            "roofline": {"bound": "hbm", "kernel": "bcjr_dequant_t16_kernel<4,2,HYB,packed>",
+                         "tensor": big[0], "achieved": achieved / 1e9, "peak": 8000.0, "unit": "GB/s",
+                         "frac": achieved / 8e12, "bytes_per_weight": 4.25},
+            "tensors": per,
+            "note": "packed 2-bit bitstreams of every tensor of one Llama-3.2-1B layer, HYB L=16 k=2 V=2"}
+
+
+def experts_estimate(torch, bcjr, dev, E, T):
+    """Expert-batched dispatch on OLMoE-1B-7B expert shapes (gate_up 2048x2048,
+    down 2048x1024; HYB L=16 k=2 V=2): E experts' 2E weights soft-quantized
+    forward + backward in one bcjr_quantize_experts call, against one
+    bcjr_quantize_weight per weight (the reference's per-expert loop).  The
+    64-expert layer time is the batched time scaled by 64 / E."""
+    import numpy as np
+    lut = np.random.default_rng(6).standard_normal((512, 2)).astype(np.float32)
+    cb = bcjr.make_hyb_codebook_gpu(lut, 9, 16, dev)
+    shapes = [(2048, 2048), (2048, 1024)] * E
+    g = torch.Generator(dev).manual_seed(11)
+    Ws = [torch.randn(s, device=dev, generator=g) * 0.02 for s in shapes]
+    gs = [torch.randn(s, device=dev, generator=g) for s in shapes]
+    sl = [torch.ones(s[0], device=dev) for s in shapes]
+    sr = [torch.ones(s[1], device=dev) for s in shapes]
+    # small warm-up of both paths (plans, LUT upload)
+    w0 = [torch.randn(64, 64, device=dev, requires_grad=True)]
+    o = bcjr.bcjr_quantize_experts(w0, [torch.ones(64, device=dev)], [torch.ones(64, device=dev)], cb, T)
+    o[0].sum().backward()
+
+    def batched():
+        lat = [w.detach().requires_grad_(True) for w in Ws]
+        outs = bcjr.bcjr_quantize_experts(lat, sl, sr, cb, T)
+        torch.autograd.backward(outs, gs)
+        return lat
+
+    def loop():
+        lat = [w.detach().requires_grad_(True) for w in Ws]
+        for w, a, b, gg in zip(lat, sl, sr, gs):
+            bcjr.bcjr_quantize_weight(w, a, b, cb, T).backward(gg)
+        return lat
+
+    res = {}
+    for name, fn in (("batched", batched), ("loop", loop)):
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize(dev)
+        res[name] = time.perf_counter() - t0
+    seqs = sum(r * c // 256 for r, c in shapes)
+    return {"experts": E, "weights": 2 * E, "sequences": seqs, "batched_seconds": res["batched"],
+            "loop_seconds": res["loop"], "speedup": res["loop"] / res["batched"],
+            "layer_64_experts_seconds": res["batched"] * 64 / E,
+            "state_updates_per_s": 4.0 * seqs * 128 * 65536 / res["batched"],
+            "note": "OLMoE-1B-7B expert shapes, HYB L=16 k=2 V=2, T=%g, forward + backward of the soft "
+                    "quantizer including both RHTs" % T}
 
 
 def calibration_copy(torch, dev):

@@ -483,6 +483,10 @@ int bcjr_decode(const bcjr_problem* prob, const int32_t* bitstream, const uint8_
   return BCJR_OK;
 }
 
+static_assert(bcjr::BITS_FMT_U8 == BCJR_BITS_U8 && bcjr::BITS_FMT_I32 == BCJR_BITS_I32 &&
+                  bcjr::BITS_FMT_PACKED == BCJR_BITS_PACKED,
+              "bitstream layout ids");
+
 int bcjr_dequant(const bcjr_problem* prob, const void* bitstream, int bits_format,
                  const int32_t* start_state, const float* codebook_or_lut, int64_t m, int64_t n, int Tx,
                  int Ty, double scale, float* out, hipStream_t stream) {
@@ -505,17 +509,36 @@ int bcjr_dequant(const bcjr_problem* prob, const void* bitstream, int bits_forma
   if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
     return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
   const int KV = prob->k * prob->V;
-  const void* fn = bcjr::dequant_kernel_ptr(KV, prob->V, prob->code);
+  const bool out16 = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  // 16x16 tiles at k = 2: one thread per tile row, aligned vector loads of its bits.
+  const size_t bits_align = bits_format == BCJR_BITS_PACKED ? 4 : 16;
+  const bool t16 = Tx == 16 && Ty == 16 && prob->k == 2 && (m * n) / 4 < (1ll << 31) && out16 &&
+                   (reinterpret_cast<uintptr_t>(bitstream) % bits_align) == 0;
+  // Vector path: 4 columns of one tile row per thread, 16-byte stores, 32-bit indices.
+  const bool vec4 = !t16 && Ty % 4 == 0 && (m * n) / 4 < (1ll << 31) && out16;
+  const void* fn = t16 ? bcjr::dequant_t16_kernel_ptr(KV, prob->V, prob->code, bits_format)
+                       : bcjr::dequant_kernel_ptr(KV, prob->V, prob->code, vec4);
   if (!fn) return fail(BCJR_EUNSUPPORTED, "no dequant kernel for k*V=%d V=%d code=%d", KV, prob->V, prob->code);
+  auto log2_or_neg = [](long long x) { return (x < 1 || (x & (x - 1))) ? -1 : __builtin_ctzll((unsigned long long)x); };
   bcjr::DqParams P = {bits_format == BCJR_BITS_I32 ? static_cast<const int32_t*>(bitstream) : nullptr,
                       bits_format == BCJR_BITS_U8 ? static_cast<const uint8_t*>(bitstream) : nullptr,
                       bits_format == BCJR_BITS_PACKED ? static_cast<const uint8_t*>(bitstream) : nullptr,
                       start_state, codebook_or_lut, out, m, n, (int)prob->N, prob->L, prob->Q, Tx, Ty,
-                      scale};
+                      log2_or_neg(Tx), log2_or_neg(Ty), log2_or_neg(n / 4),
+                      (double)(float)scale == scale ? 1 : 0, scale};
   void* args[] = {&P};
-  const long long blocks = (m * n + 255) / 256;
-  const unsigned grid = (unsigned)(blocks < 16384 ? blocks : 16384);
-  hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, stream);
+  const long long blocks = (t16 || vec4 ? m * n / 4 + 255 : m * n + 255) / 256;
+  long long cap = 16384;
+  size_t lds = 0;
+  if (t16 && prob->code == BCJR_CODE_HYB) {  // LUT staged in LDS: persistent grid
+    DeviceInfo di;
+    int rc2 = device_info(&di);
+    if (rc2) return rc2;
+    cap = (long long)di.num_cu * 8;
+    lds = (size_t)(2 << prob->Q) * sizeof(float);
+  }
+  const unsigned grid = (unsigned)(blocks < cap ? blocks : cap);
+  hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(256), args, lds, stream);
   if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel(dequant)");
   return BCJR_OK;
 }

@@ -63,7 +63,8 @@ __device__ __forceinline__ float code_3inst(uint32_t s) {
 }
 
 __device__ __forceinline__ void code_hyb(uint32_t s, const float* lut, int Q, float& c0, float& c1) {
-  const uint32_t x = s * s + s;
+  // s < 2^16 (L <= 16): the 24-bit multiply-add is exact (v_mad_u32_u24, full rate)
+  const uint32_t x = __umul24(s, s) + s;
   const uint32_t idx = (x >> (15 - Q)) & ((1u << Q) - 1u);
   c0 = lut[2 * idx];
   const float b = lut[2 * idx + 1];
@@ -346,6 +347,9 @@ struct DecParams {
   int N, L, Q;
 };
 
+// Bitstream layouts (the values of BCJR_BITS_* in the C ABI).
+enum { BITS_FMT_U8 = 0, BITS_FMT_I32 = 1, BITS_FMT_PACKED = 2 };
+
 struct DqParams {
   const int32_t* bits32;  // (B, N) one step per int32, or null
   const uint8_t* bits8;   // (B, N) one step per byte (the reference's payload), or null
@@ -355,6 +359,10 @@ struct DqParams {
   float* out;             // (m, n) row-major
   long long m, n;
   int N, L, Q, Tx, Ty;
+  int tx_shift, ty_shift; // log2 of Tx / Ty when they are powers of two, else -1
+  int n4_shift;           // log2(n / 4) when n / 4 is a power of two, else -1
+  int scale_is_f32;       // scale is a float32 value: c * scale is exact in double, so a
+                          // float32 multiply rounds it identically
   double scale;           // the product is rounded once to float32, as numpy does
 };
 

@@ -35,7 +35,8 @@ const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool internals);
 const void* bwd_kernel_ptr(int KV, int V, int code, int upt);
 const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache);
 const void* decode_kernel_ptr(int KV, int V, int code);
-const void* dequant_kernel_ptr(int KV, int V, int code);
+const void* dequant_kernel_ptr(int KV, int V, int code, bool vec4);
+const void* dequant_t16_kernel_ptr(int KV, int V, int code, int fmt);
 const void* codebook_kernel_ptr(int code);
 
 // Hadamard transforms (bcjr_rht.hip).  Rows: out[r] = scale * row_sign[r] *

@@ -333,6 +333,203 @@ __global__ __launch_bounds__(256) void bcjr_dequant_kernel(DqParams P) {
   }
 }
 
+// Vector form of bcjr_dequant_kernel for Ty % 4 == 0, m*n/4 < 2^31 and a
+// 16-byte aligned output: one thread writes 4 consecutive columns of a row with
+// one 16-byte store.  The 4 elements are 4/V consecutive steps of one tile, so
+// the state window is decoded once and then rolled forward step by step; index
+// arithmetic is 32-bit, with shifts when Tx and Ty are powers of two.
+template <int KV, int V, int CODE>
+__global__ __launch_bounds__(256) void bcjr_dequant4_kernel(DqParams P) {
+  constexpr int R = 1 << KV;
+  constexpr int NS = 4 / V;  // steps per thread
+  constexpr int per = 8 / KV;
+  const uint32_t mask = (1u << P.L) - 1u;  // L <= 16
+  const int win = (P.L + KV - 1) / KV;
+  const uint32_t n4 = (uint32_t)(P.n >> 2);
+  const uint32_t total4 = (uint32_t)((P.m * P.n) >> 2);
+  const uint32_t n_row = (uint32_t)(P.m / P.Tx);
+  const int nbytes = (P.N * KV + 7) / 8;
+  auto bits_at = [&](size_t b, int tau) -> uint32_t {
+    if (P.packed) return ((uint32_t)P.packed[b * nbytes + tau / per] >> ((tau % per) * KV)) & (R - 1);
+    if (P.bits8) return (uint32_t)P.bits8[b * P.N + tau] & (R - 1);
+    return (uint32_t)P.bits32[b * P.N + tau] & (R - 1);
+  };
+  for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < total4; q += gridDim.x * blockDim.x) {
+    const uint32_t row = q / n4;
+    const uint32_t col = (q - row * n4) << 2;
+    uint32_t rb, rr, cb, cc;
+    if (P.tx_shift >= 0) {
+      rb = row >> P.tx_shift;
+      rr = row & ((1u << P.tx_shift) - 1u);
+    } else {
+      rb = row / (uint32_t)P.Tx;
+      rr = row - rb * (uint32_t)P.Tx;
+    }
+    if (P.ty_shift >= 0) {
+      cb = col >> P.ty_shift;
+      cc = col & ((1u << P.ty_shift) - 1u);
+    } else {
+      cb = col / (uint32_t)P.Ty;
+      cc = col - cb * (uint32_t)P.Ty;
+    }
+    const size_t b = (size_t)cb * n_row + rb;
+    const int t0 = (int)(rr * (uint32_t)P.Ty + cc) / V;
+    uint32_t s = 0;
+    if (KV * (t0 + 1) < P.L) s = (uint32_t)P.start[b] << (KV * (t0 + 1));
+    for (int tau = t0 - win + 1 > 0 ? t0 - win + 1 : 0; tau <= t0; ++tau) s |= bits_at(b, tau) << (KV * (t0 - tau));
+    s &= mask;
+    float o[4];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      if (j) s = ((s << KV) | bits_at(b, t0 + j)) & mask;
+      float c[V];
+      codeword<CODE, V>(s, P.table, P.table, P.Q, c);
+#pragma unroll
+      for (int v = 0; v < V; ++v) o[j * V + v] = (float)((double)c[v] * P.scale);
+    }
+    *reinterpret_cast<float4*>(P.out + (size_t)row * P.n + col) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// The reference's tile configuration (16x16 tiles, k = 2 bits per weight, so
+// kV = 2 with V = 1 or kV = 4 with V = 2): a tile row is SR = 16 / V steps and
+// exactly 32 bits of the packed bitstream.  Each thread writes 4 consecutive
+// columns (one 16-byte store; a wave covers 1 KiB of one matrix row, so the
+// stores coalesce).  Its tile row's step indices come in one aligned load (a
+// 32-bit word packed, 8 or 16 bytes as uint8, 32 or 64 bytes as int32).
+//
+// No step-by-step replay: with g(w) the word w with the order of its kV-bit
+// groups reversed (step j of the row moves to group SR-1-j), the 64-bit value
+// H = (h << 32) | g(cur), where h is the start state for the first row of a
+// tile and g(prev) for the others (the previous row's SR >= ceil(L/kV) steps
+// fix the state), holds every state of the row: the state after step t of the
+// row is (H >> (32 - kV (t+1))) mod 2^L.  The kernel runs at a handful of VALU
+// instructions per weight: group reversal and one 64-bit shift per 4 columns, a
+// bit-field extract, the codeword and the scale per step.
+template <int FMT>
+struct RowSteps;  // step indices of one tile row, as the packed 32-bit word: word()
+
+template <>
+struct RowSteps<BITS_FMT_PACKED> {
+  uint32_t w;
+  template <int KV, int SR>
+  __device__ __forceinline__ void load(const DqParams& P, uint32_t b, int row) {
+    w = reinterpret_cast<const uint32_t*>(P.packed)[b * 16u + (uint32_t)row];  // 64 bytes per tile
+  }
+  template <int KV, int SR>
+  __device__ __forceinline__ uint32_t word() const { return w; }
+};
+
+template <>
+struct RowSteps<BITS_FMT_U8> {
+  uint32_t w[4];
+  template <int KV, int SR>
+  __device__ __forceinline__ void load(const DqParams& P, uint32_t b, int row) {
+    const uint8_t* p = P.bits8 + (size_t)(b * (uint32_t)(SR * 16) + (uint32_t)(row * SR));
+    if constexpr (SR == 16) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p);
+      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2*>(p);
+      w[0] = v.x; w[1] = v.y; w[2] = 0; w[3] = 0;
+    }
+  }
+  template <int KV, int SR>
+  __device__ __forceinline__ uint32_t word() const {  // the packed form: step j in bits [j*KV, (j+1)*KV)
+    uint32_t r = 0;
+#pragma unroll
+    for (int j = 0; j < SR; ++j) r |= ((w[j >> 2] >> ((j & 3) * 8)) & ((1u << KV) - 1u)) << (j * KV);
+    return r;
+  }
+};
+
+template <>
+struct RowSteps<BITS_FMT_I32> {
+  uint32_t w[16];
+  template <int KV, int SR>
+  __device__ __forceinline__ void load(const DqParams& P, uint32_t b, int row) {
+    const uint4* p = reinterpret_cast<const uint4*>(P.bits32 + (size_t)(b * (uint32_t)(SR * 16) + (uint32_t)(row * SR)));
+#pragma unroll
+    for (int i = 0; i < SR / 4; ++i) {
+      const uint4 v = p[i];
+      w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+  }
+  template <int KV, int SR>
+  __device__ __forceinline__ uint32_t word() const {
+    uint32_t r = 0;
+#pragma unroll
+    for (int j = 0; j < SR; ++j) r |= (w[j] & ((1u << KV) - 1u)) << (j * KV);
+    return r;
+  }
+};
+
+// Reverse the order of the KV-bit groups of a 32-bit word (KV = 2 or 4).
+template <int KV>
+__device__ __forceinline__ uint32_t reverse_groups(uint32_t w) {
+  uint32_t r = __builtin_bitreverse32(w);  // reverses groups and the bits inside them
+  r = ((r >> 1) & 0x55555555u) | ((r & 0x55555555u) << 1);  // restore bit order inside pairs
+  if constexpr (KV == 4) r = ((r >> 2) & 0x33333333u) | ((r & 0x33333333u) << 2);  // ... and nibbles
+  static_assert(KV == 2 || KV == 4, "group reversal for kV = 2 or 4");
+  return r;
+}
+
+//
+// The HYB LUT (2^Q x 2 floats, <= 32 KiB) is staged in LDS once per workgroup:
+// its lookups are random 8-byte gathers, which from global memory cost one
+// cache-line request per lane.  The grid is persistent (a few workgroups per
+// CU) so the staging is amortised.
+template <int KV, int V, int CODE, int FMT>
+__global__ __launch_bounds__(256) void bcjr_dequant_t16_kernel(DqParams P) {
+  constexpr int SR = 16 / V;  // steps per tile row
+  constexpr int SQ = SR / 4;  // steps per 4-column quarter
+  static_assert(SR * KV == 32, "k = 2: one 32-bit word of packed bits per tile row");
+  extern __shared__ __align__(16) float lds_lut[];
+  const float* table = P.table;
+  if constexpr (CODE == CODE_HYB) {
+    const int nlut = 2 << P.Q;
+    for (int i = threadIdx.x; i < nlut; i += blockDim.x) lds_lut[i] = P.table[i];
+    __syncthreads();
+    table = lds_lut;
+  }
+  const uint32_t mask = (1u << P.L) - 1u;
+  const uint32_t n4 = (uint32_t)(P.n >> 2);
+  const int n4_shift = P.n4_shift;
+  const uint32_t n_row = (uint32_t)(P.m >> 4);
+  const uint32_t total = (uint32_t)((P.m * P.n) >> 2);  // 4-column quarters
+  for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < total; q += gridDim.x * blockDim.x) {
+    const uint32_t row = n4_shift >= 0 ? q >> n4_shift : q / n4;
+    const uint32_t c4 = q - row * n4;  // column / 4
+    const int rr = (int)(row & 15u), jq = (int)(c4 & 3u);
+    const uint32_t b = (c4 >> 2) * n_row + (row >> 4);
+    RowSteps<FMT> rs;
+    rs.template load<KV, SR>(P, b, rr);
+    uint32_t hi;
+    if (rr == 0) {
+      hi = (uint32_t)P.start[b];
+    } else {
+      RowSteps<FMT> ps;
+      ps.template load<KV, SR>(P, b, rr - 1);
+      hi = reverse_groups<KV>(ps.template word<KV, SR>());
+    }
+    const uint64_t H = ((uint64_t)hi << 32) | reverse_groups<KV>(rs.template word<KV, SR>());
+    // state after the quarter's last step in the low bits; the earlier ones sit
+    // KV bits apart above it (L + KV (SQ-1) <= 22 bits)
+    const uint32_t Hq = (uint32_t)(H >> (32 - KV * SQ * (jq + 1)));
+    float o[4];
+#pragma unroll
+    for (int j = 0; j < SQ; ++j) {
+      const uint32_t s = (Hq >> (KV * (SQ - 1 - j))) & mask;
+      float c[V];
+      codeword<CODE, V>(s, table, table, P.Q, c);
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        o[j * V + v] = P.scale_is_f32 ? c[v] * (float)P.scale : (float)((double)c[v] * P.scale);
+    }
+    *reinterpret_cast<float4*>(P.out + (size_t)row * P.n + ((size_t)c4 << 2)) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // Codebook fill: one thread per state.
 template <int CODE>
 __global__ __launch_bounds__(256) void bcjr_codebook_kernel(CbParams P) {
@@ -390,9 +587,10 @@ const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache) {
 
 #define BCJR_DQ_CASE(KV_, V_, CODE_) \
   if (KV == KV_ && V == V_ && code == CODE_) \
-    return reinterpret_cast<const void*>(&bcjr_dequant_kernel<KV_, V_, CODE_>);
+    return vec4 ? reinterpret_cast<const void*>(&bcjr_dequant4_kernel<KV_, V_, CODE_>) \
+                : reinterpret_cast<const void*>(&bcjr_dequant_kernel<KV_, V_, CODE_>);
 
-const void* dequant_kernel_ptr(int KV, int V, int code) {
+const void* dequant_kernel_ptr(int KV, int V, int code, bool vec4) {
   BCJR_DQ_CASE(1, 1, CODE_TABLE)
   BCJR_DQ_CASE(2, 1, CODE_TABLE)
   BCJR_DQ_CASE(2, 1, CODE_1MAD)
@@ -404,6 +602,24 @@ const void* dequant_kernel_ptr(int KV, int V, int code) {
   BCJR_DQ_CASE(4, 1, CODE_3INST)
   BCJR_DQ_CASE(4, 2, CODE_TABLE)
   BCJR_DQ_CASE(4, 2, CODE_HYB)
+  return nullptr;
+}
+
+#define BCJR_DQ16_CASE(KV_, V_, CODE_)                                                               \
+  if (KV == KV_ && V == V_ && code == CODE_) {                                                        \
+    if (fmt == BITS_FMT_PACKED)                                                                       \
+      return reinterpret_cast<const void*>(&bcjr_dequant_t16_kernel<KV_, V_, CODE_, BITS_FMT_PACKED>); \
+    if (fmt == BITS_FMT_U8)                                                                           \
+      return reinterpret_cast<const void*>(&bcjr_dequant_t16_kernel<KV_, V_, CODE_, BITS_FMT_U8>);     \
+    return reinterpret_cast<const void*>(&bcjr_dequant_t16_kernel<KV_, V_, CODE_, BITS_FMT_I32>);      \
+  }
+
+const void* dequant_t16_kernel_ptr(int KV, int V, int code, int fmt) {
+  BCJR_DQ16_CASE(2, 1, CODE_TABLE)
+  BCJR_DQ16_CASE(2, 1, CODE_1MAD)
+  BCJR_DQ16_CASE(2, 1, CODE_3INST)
+  BCJR_DQ16_CASE(4, 2, CODE_TABLE)
+  BCJR_DQ16_CASE(4, 2, CODE_HYB)
   return nullptr;
 }
 

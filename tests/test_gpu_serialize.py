@@ -182,3 +182,16 @@ def test_dequant_empty_and_errors(bcjr_mod):
     with pytest.raises(BcjrError, match="B=3"):
         ops.dequant(spec, torch.zeros(3, dtype=torch.int32, device="cuda"), None, 32, 32, 16, 16, 1.0,
                     bitstream=torch.zeros(3, 256, dtype=torch.uint8, device="cuda"))
+
+
+@pytest.mark.parametrize("Tx,Ty,m,n", [(8, 2, 16, 6), (8, 12, 24, 36), (4, 8, 12, 40), (16, 16, 16, 16)])
+def test_dequant_tile_shapes(bcjr_mod, oracle, Tx, Ty, m, n):
+    """Tiles other than 16x16: Ty % 4 != 0 (scalar kernel), Ty not a power of two
+    (vector kernel with divisions), and a single tile."""
+    from bcjr.serialize import dequant_target_gpu
+    _say(f"dequant tiles {Tx}x{Ty} of {m}x{n}")
+    cb = _codebook(bcjr_mod, "table9v2")
+    p = _payload("table9v2", cb, m, n, seed=Tx * Ty + m, Tx=Tx, Ty=Ty)
+    ref = (oracle.dequant_unit(p["bitstreams"], p["start_states"], cb.cpu().numpy(), (m, n), 9, 4, Tx, Ty)
+           * p["W_scale"]).astype(np.float32)
+    assert np.array_equal(dequant_target_gpu(p, rotated=True, codebook=cb).cpu().numpy(), ref)
