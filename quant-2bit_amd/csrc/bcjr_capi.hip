@@ -519,15 +519,15 @@ int bcjr_dequant(const bcjr_problem* prob, const void* bitstream, int bits_forma
   const void* fn = t16 ? bcjr::dequant_t16_kernel_ptr(KV, prob->V, prob->code, bits_format)
                        : bcjr::dequant_kernel_ptr(KV, prob->V, prob->code, vec4);
   if (!fn) return fail(BCJR_EUNSUPPORTED, "no dequant kernel for k*V=%d V=%d code=%d", KV, prob->V, prob->code);
-  auto log2_or_neg = [](long long x) { return (x < 1 || (x & (x - 1))) ? -1 : __builtin_ctzll((unsigned long long)x); };
+  auto log2_or_neg = [](int x) { return (x < 1 || (x & (x - 1))) ? -1 : __builtin_ctz((unsigned)x); };
   bcjr::DqParams P = {bits_format == BCJR_BITS_I32 ? static_cast<const int32_t*>(bitstream) : nullptr,
                       bits_format == BCJR_BITS_U8 ? static_cast<const uint8_t*>(bitstream) : nullptr,
                       bits_format == BCJR_BITS_PACKED ? static_cast<const uint8_t*>(bitstream) : nullptr,
                       start_state, codebook_or_lut, out, m, n, (int)prob->N, prob->L, prob->Q, Tx, Ty,
-                      log2_or_neg(Tx), log2_or_neg(Ty), log2_or_neg(n / 4),
-                      (double)(float)scale == scale ? 1 : 0, scale};
+                      log2_or_neg(Tx), log2_or_neg(Ty), (double)(float)scale == scale ? 1 : 0, scale};
   void* args[] = {&P};
-  const long long blocks = (t16 || vec4 ? m * n / 4 + 255 : m * n + 255) / 256;
+  // t16: one workgroup per 16-row x 64-column unit; others: one thread per 4 or 1 elements
+  const long long blocks = t16 ? (m / 16) * ((n / 4 + 15) / 16) : (vec4 ? m * n / 4 + 255 : m * n + 255) / 256;
   long long cap = 16384;
   size_t lds = 0;
   if (t16 && prob->code == BCJR_CODE_HYB) {  // LUT staged in LDS: persistent grid

@@ -360,7 +360,6 @@ struct DqParams {
   long long m, n;
   int N, L, Q, Tx, Ty;
   int tx_shift, ty_shift; // log2 of Tx / Ty when they are powers of two, else -1
-  int n4_shift;           // log2(n / 4) when n / 4 is a power of two, else -1
   int scale_is_f32;       // scale is a float32 value: c * scale is exact in double, so a
                           // float32 multiply rounds it identically
   double scale;           // the product is rounded once to float32, as numpy does

@@ -394,9 +394,9 @@ __global__ __launch_bounds__(256) void bcjr_dequant4_kernel(DqParams P) {
 // The reference's tile configuration (16x16 tiles, k = 2 bits per weight, so
 // kV = 2 with V = 1 or kV = 4 with V = 2): a tile row is SR = 16 / V steps and
 // exactly 32 bits of the packed bitstream.  Each thread writes 4 consecutive
-// columns (one 16-byte store; a wave covers 1 KiB of one matrix row, so the
-// stores coalesce).  Its tile row's step indices come in one aligned load (a
-// 32-bit word packed, 8 or 16 bytes as uint8, 32 or 64 bytes as int32).
+// columns (one 16-byte store; a wave covers 256 contiguous bytes of 4 rows).  Its tile row's step indices come in one aligned load (a
+// 32-bit word packed, 8 or 16 bytes as uint8, 32 or 64 bytes as int32).  The
+// kernel needs blockDim.x == 256.
 //
 // No step-by-step replay: with g(w) the word w with the order of its kV-bit
 // groups reversed (step j of the row moves to group SR-1-j), the 64-bit value
@@ -494,14 +494,21 @@ __global__ __launch_bounds__(256) void bcjr_dequant_t16_kernel(DqParams P) {
   }
   const uint32_t mask = (1u << P.L) - 1u;
   const uint32_t n4 = (uint32_t)(P.n >> 2);
-  const int n4_shift = P.n4_shift;
   const uint32_t n_row = (uint32_t)(P.m >> 4);
-  const uint32_t total = (uint32_t)((P.m * P.n) >> 2);  // 4-column quarters
-  for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < total; q += gridDim.x * blockDim.x) {
-    const uint32_t row = n4_shift >= 0 ? q >> n4_shift : q / n4;
-    const uint32_t c4 = q - row * n4;  // column / 4
-    const int rr = (int)(row & 15u), jq = (int)(c4 & 3u);
-    const uint32_t b = (c4 >> 2) * n_row + (row >> 4);
+  // Work unit of a workgroup: one band of 16 rows x 64 columns (4 tiles), thread
+  // (tid / 16, tid % 16) -> (row in the band, 4-column quarter).  Each tile's
+  // bits are read by one workgroup only, so they are fetched into one XCD's L2
+  // once (rows of a band spread over workgroups would land on several XCDs).
+  const uint32_t nchunk = (n4 + 15u) >> 4;
+  const uint32_t units = n_row * nchunk;
+  const int rr = (int)(threadIdx.x >> 4);
+  for (uint32_t u = blockIdx.x; u < units; u += gridDim.x) {
+    const uint32_t rbnd = u / nchunk, ch = u - rbnd * nchunk;
+    const uint32_t c4 = (ch << 4) + (threadIdx.x & 15u);  // column / 4
+    if (c4 >= n4) continue;
+    const uint32_t row = (rbnd << 4) + (uint32_t)rr;
+    const int jq = (int)(c4 & 3u);
+    const uint32_t b = (c4 >> 2) * n_row + rbnd;
     RowSteps<FMT> rs;
     rs.template load<KV, SR>(P, b, rr);
     uint32_t hi;
