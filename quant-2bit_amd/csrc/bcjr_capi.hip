@@ -308,6 +308,8 @@ int launch(const Plan& pl, long long B, size_t ws_bytes, void* params, hipStream
 
 namespace {
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 int rht_impl(const float* W, float* out, int64_t batch, int64_t m, int64_t n, const float* sign_l,
              const float* sign_r, int inverse, hipStream_t stream) {
   if (batch < 0 || batch > INT32_MAX) return fail(BCJR_EINVAL, "batch=%lld outside [0, 2^31)", (long long)batch);
@@ -328,6 +330,14 @@ int rht_impl(const float* W, float* out, int64_t batch, int64_t m, int64_t n, co
   const long long rows = batch * m;
   // forward: rows of W diag(sr) H_n, then row signs, then H_m and the scale;
   // inverse: rows of W H_n then diag(sr), then H_m, row signs and the scale.
+  if (n >= 64 && aligned16(W) && aligned16(sign_r)) {  // tiled kernels: 2 passes over HBM for most shapes
+    hipError_t e = inverse
+        ? bcjr::launch_fwht_tiled(W, out, (int)batch, (int)m, (int)n, true, nullptr, sign_r, nullptr, sign_l, s,
+                                  di.num_cu * 4, stream)
+        : bcjr::launch_fwht_tiled(W, out, (int)batch, (int)m, (int)n, true, sign_r, nullptr, sign_l, nullptr, s,
+                                  di.num_cu * 4, stream);
+    return e == hipSuccess ? BCJR_OK : hip_fail(e, "bcjr_rht tiled passes");
+  }
   hipError_t e =
       inverse ? bcjr::launch_fwht_rows(W, out, rows, (int)n, nullptr, sign_r, m, nullptr, 1.0f, blocks, stream)
               : bcjr::launch_fwht_rows(W, out, rows, (int)n, sign_r, nullptr, m, sign_l, 1.0f, blocks, stream);
@@ -568,8 +578,12 @@ int bcjr_hadamard(const float* x, float* out, int64_t rows, int64_t n, float sca
   DeviceInfo di;
   int rc = device_info(&di);
   if (rc) return rc;
-  hipError_t e = bcjr::launch_fwht_rows(x, out, rows, (int)n, nullptr, nullptr, rows, nullptr, scale, di.num_cu * 8,
-                                        stream);
+  hipError_t e;
+  if (n >= 64 && rows <= INT32_MAX && aligned16(x))
+    e = bcjr::launch_fwht_tiled(x, out, 1, (int)rows, (int)n, false, nullptr, nullptr, nullptr, nullptr, scale,
+                                di.num_cu * 4, stream);
+  else
+    e = bcjr::launch_fwht_rows(x, out, rows, (int)n, nullptr, nullptr, rows, nullptr, scale, di.num_cu * 8, stream);
   return e == hipSuccess ? BCJR_OK : hip_fail(e, "bcjr_hadamard launch");
 }
 

@@ -47,6 +47,9 @@ hipError_t launch_fwht_rows(const float* x, float* out, long long rows, int n, c
                             int max_blocks, hipStream_t stream);
 hipError_t launch_fwht_cols(float* x, int batch, int m, int n, const float* row_sign, float scale,
                             int max_blocks, hipStream_t stream);
+hipError_t launch_fwht_tiled(const float* x, float* out, int batch, int m, int n, bool col, const float* pre,
+                             const float* post, const float* row_mid, const float* row_end, float scale,
+                             int max_blocks, hipStream_t stream);
 
 // LDS bytes for one workgroup.
 inline size_t fwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {
