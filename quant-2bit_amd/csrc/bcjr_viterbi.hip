@@ -31,6 +31,9 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
   constexpr int R = 1 << KV;
   constexpr int RO = R < 4 ? R : 4;
   constexpr int NSUB = R / RO;
+  // Backpointers: kV bits per reduced state when a thread's RO outputs fill a
+  // whole byte or half-word (kV = 2, 4), else one byte per state.
+  constexpr bool PACK = RO * KV == 8 || RO * KV == 16;
   static_assert(!CACHE || NSUB == 1, "codeword cache needs whole butterflies per thread");
 
   extern __shared__ __align__(16) unsigned char smem[];
@@ -69,6 +72,7 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
     }
   }
 
+  const int row_bytes = PACK ? (NT * KV) >> 3 : NT;  // backpointer bytes per step
   for (long long b = blockIdx.x; b < P.B; b += gridDim.x) {
     uint8_t* bp = P.ws + (size_t)blockIdx.x * (size_t)N * (size_t)NT;
     const float* seqb = P.seq + (size_t)b * N * V;
@@ -123,12 +127,23 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
             ro[r] = best;
             bpw |= (uint32_t)bi << (8 * r);
           }
-          float* o = cur + R * u + sub * RO;
+          store_vec<RO>(cur + R * u + sub * RO, ro);
+          if constexpr (PACK) {  // entries R*u + sub*RO .. +RO-1 at kV bits each
+            uint32_t bits = 0;
 #pragma unroll
-          for (int r = 0; r < RO; ++r) o[r] = ro[r];
-          uint8_t* bdst = bp + (size_t)t * NT + R * u + sub * RO;
+            for (int r = 0; r < RO; ++r) bits |= ((bpw >> (8 * r)) & (R - 1)) << (r * KV);
+            uint8_t* row = bp + (size_t)t * row_bytes;
+            const int e0 = R * u + sub * RO;
+            if constexpr (RO * KV == 8) {
+              row[(e0 * KV) >> 3] = (uint8_t)bits;
+            } else {
+              *reinterpret_cast<uint16_t*>(row + ((e0 * KV) >> 3)) = (uint16_t)bits;
+            }
+          } else {
+            uint8_t* bdst = bp + (size_t)t * NT + R * u + sub * RO;
 #pragma unroll
-          for (int r = 0; r < RO; ++r) bdst[r] = (uint8_t)(bpw >> (8 * r));
+            for (int r = 0; r < RO; ++r) bdst[r] = (uint8_t)(bpw >> (8 * r));
+          }
         }
       }
       __syncthreads();
@@ -194,24 +209,31 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
     // predecessor of the states of step t+1, so walk_{t} = bp_t(walk_{t+1} >> kV)
     // * NT + (walk_{t+1} >> kV).  Rows are staged in LDS, up to 8 at a time, and
     // walked on one thread.
-    const int cap = (int)((2 * (size_t)NT * sizeof(float)) / (size_t)NT);
+    const int cap = (int)((2 * (size_t)NT * sizeof(float)) / (size_t)row_bytes);
     uint8_t* stage = reinterpret_cast<uint8_t*>(rbuf);
     int s = walkbuf[N - 1];
     for (int hi = N - 2; hi >= 0; hi -= cap) {
       const int lo = max(0, hi - cap + 1);
-      const int nbytes_rows = (hi - lo + 1) * NT;
-      if ((NT & 3) == 0) {
-        const uint32_t* srcw = reinterpret_cast<const uint32_t*>(bp + (size_t)lo * NT);
+      const int nbytes_rows = (hi - lo + 1) * row_bytes;
+      if ((row_bytes & 3) == 0) {
+        const uint32_t* srcw = reinterpret_cast<const uint32_t*>(bp + (size_t)lo * row_bytes);
         uint32_t* dstw = reinterpret_cast<uint32_t*>(stage);
         for (int i = tid; i < (nbytes_rows >> 2); i += nthr) dstw[i] = srcw[i];
       } else {
-        for (int i = tid; i < nbytes_rows; i += nthr) stage[i] = bp[(size_t)lo * NT + i];
+        for (int i = tid; i < nbytes_rows; i += nthr) stage[i] = bp[(size_t)lo * row_bytes + i];
       }
       __syncthreads();
       if (tid == 0) {
         for (int t = hi; t >= lo; --t) {
           const int j = s >> KV;
-          s = (int)stage[(size_t)(t - lo) * NT + j] * NT + j;
+          const uint8_t* row = stage + (size_t)(t - lo) * row_bytes;
+          int p;
+          if constexpr (PACK) {
+            p = (row[(j * KV) >> 3] >> ((j * KV) & 7)) & (R - 1);
+          } else {
+            p = row[j];
+          }
+          s = p * NT + j;
           walkbuf[t] = s;
         }
       }
