@@ -22,6 +22,8 @@ Also reported:
   * dequantization of one Llama-3.2-1B layer from the packed 2-bit format
     (bcjr_dequant + inverse RHT per tensor), with the dequant kernel's HBM
     roofline;
+  * seconds per Llama-3.2-1B MLP-block QAT step (196,608 sequences at T), from
+    the timed step;
   * the expert-batched dispatch on OLMoE-1B-7B expert shapes against the
     per-weight loop, and the 64-expert layer time it implies;
   * the CPU oracle (C/OpenMP) timed on a bounded sample of the same workload.
@@ -56,6 +58,7 @@ LAYER_TENSORS = (("q", 2048, 2048, 0.05), ("k", 512, 2048, 0.08), ("v", 512, 204
                  ("o", 2048, 2048, 0.2), ("gate", 8192, 2048, 0.3), ("up", 8192, 2048, 0.4),
                  ("down", 2048, 8192, 0.5))
 LAYER_SEQS = sum(r * c // 256 for _, r, c, _ in LAYER_TENSORS)  # 237,568
+MLP_SEQS = 3 * 8192 * 2048 // 256  # gate, up, down: 196,608
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "bcjr_tile_hbm_traffic.txt")
 CALIB_BYTES = 256 << 20
 
@@ -242,6 +245,8 @@ def main():
         "dtype": "f32", "data": "synthetic N(0,1) sequences (seed 0), upstream gradient N(0,1) (seed 1)",
         "config": {"workload": workload, "L": L, "k": k, "V": V, "N": N, "B": B, "code": kind, "T": args.T},
         "layer_step_s": layer["seconds"] if layer else None,
+        # Llama-3.2-1B MLP block (gate/up 8192x2048, down 2048x8192: 196,608 sequences) at T
+        "mlp_block_step_s": (ms_step / 1e3) * MLP_SEQS / B if args.config == "tile" else None,
         "layer": layer,
         "roofline": roofline, "kernels": kernels,
         "dequant": dequant, "experts": experts,
@@ -375,35 +380,37 @@ def dequant_estimate(torch, bcjr, ops, dev):
 
 
 def experts_estimate(torch, bcjr, dev, E, T):
-    """Expert-batched dispatch on OLMoE-1B-7B expert shapes (gate_up 2048x2048,
-    down 2048x1024; HYB L=16 k=2 V=2): E experts' 2E weights soft-quantized
-    forward + backward in one bcjr_quantize_experts call, against one
-    bcjr_quantize_weight per weight (the reference's per-expert loop).  The
+    """Expert-batched dispatch on OLMoE-1B-7B expert shapes (gate 1024x2048,
+    up 1024x2048, down 2048x1024 per expert; N(0,1) weights times a lognormal
+    (sigma 0.5) scale per expert; L=16, k=2, V=1, 3INST): E experts' 3E weights
+    soft-quantized forward + backward in one bcjr_quantize_experts call, against
+    one bcjr_quantize_weight per weight (the reference's per-expert loop).  The
     64-expert layer time is the batched time scaled by 64 / E."""
     import numpy as np
-    lut = np.random.default_rng(6).standard_normal((512, 2)).astype(np.float32)
-    cb = bcjr.make_hyb_codebook_gpu(lut, 9, 16, dev)
-    shapes = [(2048, 2048), (2048, 1024)] * E
+    cb = bcjr.make_3inst_codebook(16, dev)
+    kw = dict(L=16, k=2, V=1)
+    shapes = [(1024, 2048), (1024, 2048), (2048, 1024)] * E
+    scales = np.exp(np.random.default_rng(7).normal(0.0, 0.5, E)).repeat(3)
     g = torch.Generator(dev).manual_seed(11)
-    Ws = [torch.randn(s, device=dev, generator=g) * 0.02 for s in shapes]
+    Ws = [torch.randn(s, device=dev, generator=g) * float(sc) for s, sc in zip(shapes, scales)]
     gs = [torch.randn(s, device=dev, generator=g) for s in shapes]
     sl = [torch.ones(s[0], device=dev) for s in shapes]
     sr = [torch.ones(s[1], device=dev) for s in shapes]
     # small warm-up of both paths (plans, LUT upload)
     w0 = [torch.randn(64, 64, device=dev, requires_grad=True)]
-    o = bcjr.bcjr_quantize_experts(w0, [torch.ones(64, device=dev)], [torch.ones(64, device=dev)], cb, T)
+    o = bcjr.bcjr_quantize_experts(w0, [torch.ones(64, device=dev)], [torch.ones(64, device=dev)], cb, T, **kw)
     o[0].sum().backward()
 
     def batched():
         lat = [w.detach().requires_grad_(True) for w in Ws]
-        outs = bcjr.bcjr_quantize_experts(lat, sl, sr, cb, T)
+        outs = bcjr.bcjr_quantize_experts(lat, sl, sr, cb, T, **kw)
         torch.autograd.backward(outs, gs)
         return lat
 
     def loop():
         lat = [w.detach().requires_grad_(True) for w in Ws]
         for w, a, b, gg in zip(lat, sl, sr, gs):
-            bcjr.bcjr_quantize_weight(w, a, b, cb, T).backward(gg)
+            bcjr.bcjr_quantize_weight(w, a, b, cb, T, **kw).backward(gg)
         return lat
 
     res = {}
@@ -414,12 +421,14 @@ def experts_estimate(torch, bcjr, dev, E, T):
         torch.cuda.synchronize(dev)
         res[name] = time.perf_counter() - t0
     seqs = sum(r * c // 256 for r, c in shapes)
-    return {"experts": E, "weights": 2 * E, "sequences": seqs, "batched_seconds": res["batched"],
+    return {"experts": E, "weights": 3 * E, "sequences": seqs, "batched_seconds": res["batched"],
             "loop_seconds": res["loop"], "speedup": res["loop"] / res["batched"],
             "layer_64_experts_seconds": res["batched"] * 64 / E,
-            "state_updates_per_s": 4.0 * seqs * 128 * 65536 / res["batched"],
-            "note": "OLMoE-1B-7B expert shapes, HYB L=16 k=2 V=2, T=%g, forward + backward of the soft "
-                    "quantizer including both RHTs" % T}
+            "layer_64_experts_sequences": seqs * 64 // E,
+            "state_updates_per_s": 4.0 * seqs * 256 * 65536 / res["batched"],
+            "note": "OLMoE-1B-7B expert shapes (gate, up 1024x2048, down 2048x1024), lognormal per-expert "
+                    "scales, 3INST L=16 k=2 V=1, T=%g, forward + backward of the soft quantizer including "
+                    "both RHTs" % T}
 
 
 def calibration_copy(torch, dev):
