@@ -323,6 +323,36 @@ def test_full_size_properties(bcjr_mod):
     assert float(diff.median()) < 1e-4
 
 
+def test_bench_batch_spot_check_vs_oracle(bcjr_mod, oracle):
+    """The single-tile workload at its full size (B=4096: each workgroup reuses its
+    HBM slot for ~16 sequences): four sequences of the batch, first, middle and
+    last, against the oracle -- soft, log Z and gradient at T=0.1, and the
+    Viterbi path bit-exact."""
+    _say("bench batch spot check B=4096")
+    from bcjr import bcjr_forward_backward, make_3inst_codebook, viterbi_encode_v_batched_hip
+    B, N, L = 4096, 256, 16
+    rng = np.random.default_rng(0)
+    seq = rng.standard_normal((B, N, 1)).astype(np.float32)
+    g = rng.standard_normal((B, N, 1)).astype(np.float32)
+    cb = make_3inst_codebook(L, "cuda")
+    cb_np = cb.cpu().numpy()
+    x = torch.tensor(seq, device="cuda", requires_grad=True)
+    soft, logZ = bcjr_forward_backward(x, cb, 0.1, L=L, k=2, V=1)
+    (soft * torch.tensor(g, device="cuda")).sum().backward()
+    bits, start, recon, _, out = viterbi_encode_v_batched_hip(x.detach()[:, :, 0].contiguous(), cb, L=L, k=2, V=1,
+                                                              return_all=True)
+    pick = [0, 1, 2047, 4095]
+    s_ref, z_ref = oracle.bcjr_forward(seq[pick], cb_np, 0.1, L, 2)
+    d_ref = oracle.bcjr_backward(seq[pick], cb_np, 0.1, L, 2, g[pick])
+    assert max_rel(soft.detach().cpu().numpy()[pick], s_ref) < SOFT_TOL
+    assert np.abs(logZ.detach().cpu().numpy()[pick] - z_ref).max() <= LOGZ_TOL * np.abs(z_ref).max()
+    assert max_rel(x.grad.cpu().numpy()[pick], d_ref) < GRAD_TOL
+    walk_r, bits_r, start_r, recon_r, _ = oracle.viterbi(seq[pick], cb_np, L, 2)
+    assert (out["walk"].cpu().numpy()[pick] == walk_r).all()
+    assert (bits.cpu().numpy()[pick] == bits_r).all() and (start.cpu().numpy()[pick] == start_r).all()
+    assert (recon.cpu().numpy()[pick] == recon_r.reshape(len(pick), N)).all()
+
+
 def test_low_temperature_precision_bound(bcjr_mod, oracle):
     """Below T = 1e-2 float32 log-domain recursions lose precision as 1/T (the
     alpha/beta of a state on the final best path can lie ~1e4/T log2-units below
