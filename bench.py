@@ -24,6 +24,7 @@ Also reported:
     roofline;
   * seconds per Llama-3.2-1B MLP-block QAT step (196,608 sequences at T), from
     the timed step;
+  * the reference QAT shape (L=16, V=2, N=128, HYB) as a secondary config;
   * the expert-batched dispatch on OLMoE-1B-7B expert shapes against the
     per-weight loop, and the 64-expert layer time it implies;
   * the CPU oracle (C/OpenMP) timed on a bounded sample of the same workload.
@@ -74,6 +75,8 @@ def parse():
     ap.add_argument("--cpu-sample", type=int, default=256, help="sequences in the CPU baseline sample")
     ap.add_argument("--no-layer", action="store_true", help="skip the per-temperature layer estimate")
     ap.add_argument("--no-dequant", action="store_true", help="skip the dequant (on-disk format) leg")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the reference QAT shape (L=16, V=2, N=128, HYB) leg")
     ap.add_argument("--experts", type=int, default=2,
                     help="OLMoE experts in the expert-batched dispatch leg (0 skips it)")
     return ap.parse_args()
@@ -227,6 +230,9 @@ def main():
     layer = None
     if args.config == "tile" and not args.no_layer:
         layer = layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev)
+    secondary = None
+    if args.config == "tile" and not args.no_secondary:
+        secondary = secondary_config(torch, bcjr, ops, dev, exp_peak, args.T)
     dequant = None
     if args.config == "tile" and not args.no_dequant:
         dequant = dequant_estimate(torch, bcjr, ops, dev)
@@ -249,7 +255,7 @@ def main():
         "mlp_block_step_s": (ms_step / 1e3) * MLP_SEQS / B if args.config == "tile" else None,
         "layer": layer,
         "roofline": roofline, "kernels": kernels,
-        "dequant": dequant, "experts": experts,
+        "secondary": secondary, "dequant": dequant, "experts": experts,
         "peaks_per_s": {k_: v["per_s"] for k_, v in peaks.items()},
         "cpu_baseline": cpu,
     }
@@ -326,6 +332,43 @@ def layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev):
             "note": "fwd+bwd per tensor timed on a %d-sequence batch at that tensor's T, scaled by its "
                     "sequence count, plus one Viterbi pack of every tile and four random Hadamard "
                     "transforms per tensor" % B}
+
+
+def secondary_config(torch, bcjr, ops, dev, exp_peak, T, B=4096):
+    """The reference QAT shape as a secondary config: L=16, k=2, V=2 (kV=4), N=128
+    steps, HYB codebook (random 2^9 x 2 LUT), B sequences of N(0,1) weights:
+    forward + backward of the node, per-launch durations from HIP events, and
+    the roofline at 5 + 2 * 2^-4 algorithmic transcendentals per cell."""
+    import numpy as np
+    L, k, V, N = 16, 2, 2, 128
+    lut = np.random.default_rng(3).standard_normal((512, 2)).astype(np.float32)
+    cb = bcjr.make_hyb_codebook_gpu(lut, 9, L, dev)
+    spec, table = bcjr.forward_backward._spec_for(cb, L, k, V)
+    x = torch.randn(B, N, V, device=dev, generator=torch.Generator(dev).manual_seed(4))
+    g = torch.randn(B, N, V, device=dev, generator=torch.Generator(dev).manual_seed(5))
+    stream = torch.cuda.current_stream(dev)
+    ops.forward(spec, x, T, table)
+    ops.backward(spec, x, T, table, g)
+    reps = 3
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    e[0].record(stream)
+    for _ in range(reps):
+        ops.forward(spec, x, T, table)
+    e[1].record(stream)
+    for _ in range(reps):
+        ops.backward(spec, x, T, table, g)
+    e[2].record(stream)
+    torch.cuda.synchronize(dev)
+    fwd_s = e[0].elapsed_time(e[1]) / 1e3 / reps
+    bwd_s = e[1].elapsed_time(e[2]) / 1e3 / reps
+    cells = float(B) * N * (1 << L)
+    per_cell = trans_per_cell_grad(k * V)
+    return {"workload": "reference QAT shape: L=16 k=2 V=2 (kV=4) N=128 B=%d, HYB, T=%g" % (B, T),
+            "fwd_ms": fwd_s * 1e3, "bwd_ms": bwd_s * 1e3,
+            "state_updates_per_s": 4.0 * cells / (fwd_s + bwd_s),
+            "roofline": {"bound": "valu_exp", "achieved": per_cell * cells / (fwd_s + bwd_s) / 1e12,
+                         "peak": exp_peak / 1e12, "unit": "Texp/s",
+                         "frac": per_cell * cells / (fwd_s + bwd_s) / exp_peak, "per_cell": per_cell}}
 
 
 def dequant_estimate(torch, bcjr, ops, dev):
