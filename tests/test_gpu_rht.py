@@ -198,3 +198,49 @@ def test_ptq_residual_definition(bcjr_mod):
     assert abs(ssq - ref) <= 1e-5 * ref
     # 2-bit 3INST on unit-variance Gaussians: MSE in the published band (QTIP Table 1 ~0.069)
     assert 0.04 < ssq / cnt < 0.12
+
+
+def test_rht_and_dequant_capture_replays(bcjr_mod, oracle):
+    """The RHT (single and batched) and the dequant kernel captured in one HIP
+    graph replay to the eager results, with eager work between replays (the
+    entry points are stream-ordered and allocate nothing)."""
+    _say("rht + dequant graph capture")
+    from bcjr import ops
+    from bcjr.serialize import pack_bitstreams
+    m, n = 256, 512
+    rng = np.random.default_rng(21)
+    W = torch.tensor(rng.standard_normal((m, n)).astype(np.float32), device="cuda")
+    Wb = torch.tensor(rng.standard_normal((3, 64, 128)).astype(np.float32), device="cuda")
+    sl, sr = torch.tensor(_signs(m, 1), device="cuda"), torch.tensor(_signs(n, 2), device="cuda")
+    slb = torch.tensor(np.stack([_signs(64, 3 + e) for e in range(3)]), device="cuda")
+    srb = torch.tensor(np.stack([_signs(128, 9 + e) for e in range(3)]), device="cuda")
+    B = (m // 16) * (n // 16)
+    bits = rng.integers(0, 16, (B, 128)).astype(np.uint8)
+    packed = torch.tensor(pack_bitstreams(bits, 4), device="cuda")
+    start = torch.tensor(rng.integers(0, 1 << 16, B).astype(np.int32), device="cuda")
+    lut = np.random.default_rng(2).standard_normal((512, 2)).astype(np.float32)
+    cb = bcjr_mod.make_hyb_codebook_gpu(lut, 9, 16, "cuda")
+    spec = ops.Spec(16, 2, 2, ops.CODE_HYB, 9)
+
+    def work():
+        a = bcjr_mod.apply_rht_gpu(W, sl, sr)
+        b = bcjr_mod.apply_inverse_rht_batched(Wb, slb, srb)
+        c = ops.dequant(spec, start, cb._bcjr_lut, m, n, 16, 16, 0.03, packed=packed)
+        return a, b, bcjr_mod.apply_inverse_rht_gpu(c, sl, sr)
+
+    ref = [t.clone() for t in work()]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            work()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = work()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, ref):
+            assert torch.equal(o, r)
+        _ = torch.randn(4096, device="cuda").sum().item()  # eager work between replays
