@@ -9,7 +9,7 @@ from .forward_backward import (  # noqa: F401
 )
 from .codes import make_1mad_codebook, make_3inst_codebook, make_hyb_codebook_gpu  # noqa: F401
 from .viterbi import (  # noqa: F401
-    viterbi_decode_v_batched, viterbi_encode_chunked, viterbi_encode_v_batched_hip,
+    viterbi_decode_v_batched, viterbi_encode_chunked, viterbi_encode_v_batched_cuda, viterbi_encode_v_batched_hip,
 )
 from .quant import (  # noqa: F401
     bcjr_quantize_tiles, bcjr_quantize_weight, bcjr_quantize_weight_rotated, tile_for_viterbi, untile_from_viterbi,
@@ -21,7 +21,7 @@ from .rht import (  # noqa: F401
 from .experts import bcjr_quantize_experts, quantize_moe_experts  # noqa: F401
 from .ste import (  # noqa: F401
     TrellisQuantSTE, TrellisQuantSTE_IP, ptq_residual, quantize_forward_gpu, quantize_forward_gpu_no_rht,
-    replay_walks,
+    quantize_forward_numpy, replay_walks,
 )
 from .serialize import (  # noqa: F401
     dequant_target, dequant_target_gpu, load_packed, load_quantized, pack_bitstreams, precompute_walk_states,

@@ -1,7 +1,8 @@
 """Hard straight-through trellis quantizer on the gfx950 Viterbi kernel.
 
 Drop-in for src/qat/ste.py:160-357: quantize_forward_gpu_no_rht,
-quantize_forward_gpu, TrellisQuantSTE, TrellisQuantSTE_IP and _replay_walks.
+quantize_forward_gpu, quantize_forward_numpy, TrellisQuantSTE, TrellisQuantSTE_IP
+and _replay_walks.
 Data flow per weight: RHT (unless already rotated) -> RMS scale -> 16x16 tiles
 -> Viterbi reconstruction -> untile -> rescale -> inverse RHT; the backward is
 the identity (straight-through).  Every step runs on the GPU: the RHT on the FWHT
@@ -55,6 +56,33 @@ def quantize_forward_gpu(W_latent, sign_l_gpu, sign_r_gpu, codebook_gpu, Tx=TX, 
     W_tilde = apply_rht_gpu(W_latent, sign_l_gpu, sign_r_gpu)
     W_tilde_q = quantize_forward_gpu_no_rht(W_tilde, codebook_gpu, Tx, Ty, k)
     return apply_inverse_rht_gpu(W_tilde_q, sign_l_gpu, sign_r_gpu)
+
+
+def quantize_forward_numpy(W_latent_np, sign_l_np, sign_r_np, codebook_gpu, Tx=TX, Ty=TY, k=K_BITS):
+    """Numpy in, numpy out (src/qat/ste.py:213-267): RHT -> RMS scale -> tiles ->
+    Viterbi -> untile -> rescale -> inverse RHT.  The transforms and the Viterbi
+    run on the GPU kernels; the scale is the reference's numpy float32 RMS of the
+    rotated weight.  Returns (W_q (m, n) float32, W_scale, walks (B, N) int64,
+    bitstreams (B, N) int32, start_states (B,) int32)."""
+    dev = codebook_gpu.device
+    L, V = _lv(codebook_gpu)
+    W = torch.from_numpy(np.ascontiguousarray(W_latent_np, dtype=np.float32)).to(dev)
+    sl = torch.from_numpy(np.ascontiguousarray(sign_l_np, dtype=np.float32)).to(dev)
+    sr = torch.from_numpy(np.ascontiguousarray(sign_r_np, dtype=np.float32)).to(dev)
+    with torch.no_grad():
+        W_tilde = apply_rht_gpu(W, sl, sr).cpu().numpy()
+        W_scale = float(np.sqrt((W_tilde ** 2).mean()))
+        if W_scale < 1e-30:
+            W_scale = 1.0
+        unit = torch.from_numpy(W_tilde / W_scale).to(dev)
+        m, n = unit.shape
+        seqs, info = tile_for_viterbi(unit, Tx, Ty)
+        bits, start, recons, _ = viterbi_encode_v_batched_hip(seqs.contiguous(), codebook_gpu, L=L, k=k, V=V)
+        W_tilde_q = untile_from_viterbi(recons, info, (m, n), Tx, Ty).cpu().numpy() * W_scale
+        W_q = apply_inverse_rht_gpu(torch.from_numpy(W_tilde_q.astype(np.float32)).to(dev), sl, sr).cpu().numpy()
+    bits_np, start_np = bits.cpu().numpy(), start.cpu().numpy()
+    walks = replay_walks(bits_np.astype(np.int64), start_np.astype(np.int64), L=L, kV=k * V)
+    return W_q.astype(np.float32), W_scale, walks, bits_np, start_np
 
 
 def _f32_cuda(x, device):
@@ -126,5 +154,5 @@ def ptq_residual(W_latent, sign_l, sign_r, codebook_gpu):
         return float(diff.pow(2).sum()), diff.numel()
 
 
-__all__ = ["quantize_forward_gpu_no_rht", "quantize_forward_gpu", "TrellisQuantSTE", "TrellisQuantSTE_IP",
-           "replay_walks", "ptq_residual"]
+__all__ = ["quantize_forward_gpu_no_rht", "quantize_forward_gpu", "quantize_forward_numpy", "TrellisQuantSTE",
+           "TrellisQuantSTE_IP", "replay_walks", "ptq_residual"]

@@ -41,6 +41,20 @@ def viterbi_encode_v_batched_hip(sequences, codebook, L=16, k=2, V=2, return_all
     return res
 
 
+def viterbi_encode_v_batched_cuda(sequences, codebook):
+    """The reference's entry point (src/viterbi/cuda_kernel.py:166-220), fixed at
+    L=16, k=2, V=2: sequences (B, T) float32 GPU tensor with T even, codebook
+    (65536, 2).  Returns (bitstreams (B, T/2) int32, start_states (B,) int32,
+    recons (B, T) float32, mses (B,) float32)."""
+    if not (sequences.is_cuda and codebook.is_cuda):
+        raise AssertionError("sequences and codebook must be GPU tensors")
+    if tuple(codebook.shape) != (65536, 2):
+        raise AssertionError(f"codebook must be (65536, 2); got {tuple(codebook.shape)}")
+    if sequences.dim() != 2 or sequences.shape[1] % 2:
+        raise AssertionError(f"sequences must be (B, T) with T even; got {tuple(sequences.shape)}")
+    return viterbi_encode_v_batched_hip(sequences, codebook, L=16, k=2, V=2)
+
+
 def viterbi_encode_chunked(sequences, codebook, chunk=None, L=16, k=2, V=2):
     """Same contract as src/qat/ste.py:58-73.  The engine's memory use is bounded
     by its workspace, so the whole batch runs in one launch unless chunk is set."""
@@ -59,4 +73,5 @@ def viterbi_decode_v_batched(bitstreams, start_states, codebook, L=16, k=2, V=2,
     return walk, recon.reshape(walk.shape[0], -1)
 
 
-__all__ = ["viterbi_encode_v_batched_hip", "viterbi_encode_chunked", "viterbi_decode_v_batched"]
+__all__ = ["viterbi_encode_v_batched_hip", "viterbi_encode_v_batched_cuda", "viterbi_encode_chunked",
+           "viterbi_decode_v_batched"]

@@ -244,3 +244,38 @@ def test_rht_and_dequant_capture_replays(bcjr_mod, oracle):
         for o, r in zip(outs, ref):
             assert torch.equal(o, r)
         _ = torch.randn(4096, device="cuda").sum().item()  # eager work between replays
+
+
+def test_reference_named_viterbi_and_numpy_ste(bcjr_mod, oracle):
+    """viterbi_encode_v_batched_cuda keeps the reference's fixed-shape contract
+    (src/viterbi/cuda_kernel.py:166-220); quantize_forward_numpy
+    (src/qat/ste.py:213-267) against the same steps on the oracle, bit for bit
+    (m*n an even power of two, numpy float32 RMS as the reference computes it)."""
+    _say("reference-named viterbi + numpy STE")
+    from bcjr.quant import tile_for_viterbi, untile_from_viterbi
+    lut = np.random.default_rng(2).standard_normal((512, 2)).astype(np.float32)
+    cb = bcjr_mod.make_hyb_codebook_gpu(lut, 9, 16, "cuda")
+    x = torch.randn(8, 256, device="cuda")
+    a = bcjr_mod.viterbi_encode_v_batched_cuda(x, cb)
+    b = bcjr_mod.viterbi_encode_v_batched_hip(x, cb, L=16, k=2, V=2)
+    assert all(torch.equal(p, q) for p, q in zip(a, b))
+    with pytest.raises(AssertionError):
+        bcjr_mod.viterbi_encode_v_batched_cuda(x, torch.zeros(4096, 2, device="cuda"))
+    with pytest.raises(AssertionError):
+        bcjr_mod.viterbi_encode_v_batched_cuda(x[:, :255], cb)
+
+    m, n = 64, 256
+    rng = np.random.default_rng(17)
+    W = (rng.standard_normal((m, n)) * 0.03).astype(np.float32)
+    sl, sr = _signs(m, 31), _signs(n, 32)
+    W_q, W_scale, walks, bits, start = bcjr_mod.quantize_forward_numpy(W, sl, sr, cb)
+    Wt = oracle.rht(W, sl, sr)
+    scale = float(np.sqrt((Wt ** 2).mean()))
+    assert W_scale == scale
+    seqs, info = tile_for_viterbi(torch.tensor(Wt / scale), 16, 16)
+    walk_r, bits_r, start_r, recon_r, _ = oracle.viterbi(seqs.numpy().reshape(seqs.shape[0], -1, 2), cb.cpu().numpy(),
+                                                          16, 4)
+    assert (bits == bits_r).all() and (start == start_r).all()
+    assert (walks == walk_r.astype(np.int64)).all()
+    Wtq = untile_from_viterbi(torch.tensor(recon_r.reshape(seqs.shape[0], -1)), info, (m, n), 16, 16).numpy() * scale
+    assert np.array_equal(W_q, oracle.inverse_rht(Wtq.astype(np.float32), sl, sr))
