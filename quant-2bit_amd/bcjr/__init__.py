@@ -18,10 +18,10 @@ from .rht import (  # noqa: F401
     apply_inverse_rht_batched, apply_inverse_rht_gpu, apply_rht_batched, apply_rht_gpu, hadamard_transform,
     make_sign_vector,
 )
-from .experts import bcjr_quantize_experts, quantize_moe_experts  # noqa: F401
+from .experts import bcjr_quantize_experts, quantize_moe_experts, ste_quantize_experts  # noqa: F401
 from .ste import (  # noqa: F401
     TrellisQuantSTE, TrellisQuantSTE_IP, ptq_residual, quantize_forward_gpu, quantize_forward_gpu_no_rht,
-    quantize_forward_numpy, replay_walks,
+    measure_ptq_residual, quantize_forward_numpy, replay_walks,
 )
 from .serialize import (  # noqa: F401
     dequant_target, dequant_target_gpu, load_packed, load_quantized, pack_bitstreams, precompute_walk_states,

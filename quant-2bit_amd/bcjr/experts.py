@@ -25,6 +25,7 @@ import torch
 from .forward_backward import K_BITS, L_BITS, V_DIM, bcjr_forward_backward
 from .quant import TX, TY
 from .rht import apply_inverse_rht_batched, apply_rht_batched
+from .viterbi import viterbi_encode_v_batched_hip
 
 
 def _per_weight_T(T_temps, E, device):
@@ -99,6 +100,49 @@ def bcjr_quantize_experts(W_latents, sign_l, sign_r, codebook, T_temps, Tx=TX, T
     return out
 
 
+def ste_quantize_experts(W_latents, sign_l, sign_r, codebook, Tx=TX, Ty=TY, k=K_BITS):
+    """Hard (T -> 0) quantization of E weights in one Viterbi launch: what
+    quantize_forward_gpu (src/qat/ste.py:183-212) gives each weight, for a whole
+    layer at once (QATMoELayer.prime_cache, src/qat/qat_moe_layer.py:129-135,
+    loops experts instead).  No gradient: this primes caches and packs."""
+    E = len(W_latents)
+    if not (len(sign_l) == len(sign_r) == E):
+        raise AssertionError(f"{E} weights but {len(sign_l)} / {len(sign_r)} sign vectors")
+    if E == 0:
+        return []
+    S, V = codebook.shape
+    L = int(S).bit_length() - 1
+    device = W_latents[0].device
+    groups: "OrderedDict[tuple, list]" = OrderedDict()
+    for e, W in enumerate(W_latents):
+        m, n = W.shape
+        if m % Tx or n % Ty:
+            raise AssertionError(f"weight {e} shape {(m, n)} not tileable by {(Tx, Ty)}")
+        groups.setdefault((m, n), []).append(e)
+    seqs, meta = [], []
+    with torch.no_grad():
+        for (m, n), idx in groups.items():
+            G = len(idx)
+            W = torch.stack([W_latents[e].detach().float() for e in idx])
+            SL = torch.stack([torch.as_tensor(sign_l[e], device=device, dtype=torch.float32) for e in idx])
+            SR = torch.stack([torch.as_tensor(sign_r[e], device=device, dtype=torch.float32) for e in idx])
+            Wt = apply_rht_batched(W, SL, SR)
+            scale = Wt.pow(2).mean(dim=(1, 2)).sqrt().clamp(min=1e-30)
+            n_col = n // Ty
+            s = (Wt / scale[:, None, None]).reshape(G, m, n_col, Ty).permute(0, 2, 1, 3).reshape(-1, Tx * Ty)
+            seqs.append(s)
+            meta.append(((m, n), idx, SL, SR, scale, s.shape[0]))
+        _, _, recon, _ = viterbi_encode_v_batched_hip(torch.cat(seqs).contiguous(), codebook, L=L, k=k, V=V)
+        out = [None] * E
+        for ((m, n), idx, SL, SR, scale, B), rec in zip(meta, torch.split(recon, [mm[-1] for mm in meta])):
+            G = len(idx)
+            q = rec.reshape(G, n // Ty, m, Ty).permute(0, 2, 1, 3).reshape(G, m, n) * scale[:, None, None]
+            Wq = apply_inverse_rht_batched(q, SL, SR)
+            for j, e in enumerate(idx):
+                out[e] = Wq[j]
+    return out
+
+
 def quantize_moe_experts(experts_weights, signs, codebook, T_temps, **kw):
     """Dict form for a layer: experts_weights maps a name (e.g. (expert, "gate_up"))
     to its latent weight, signs maps the same names to (sign_l, sign_r); returns a
@@ -112,4 +156,4 @@ def quantize_moe_experts(experts_weights, signs, codebook, T_temps, **kw):
     return dict(zip(names, outs))
 
 
-__all__ = ["bcjr_quantize_experts", "quantize_moe_experts"]
+__all__ = ["bcjr_quantize_experts", "ste_quantize_experts", "quantize_moe_experts"]

@@ -154,5 +154,28 @@ def ptq_residual(W_latent, sign_l, sign_r, codebook_gpu):
         return float(diff.pow(2).sum()), diff.numel()
 
 
+def _quantized_linears(layer):
+    """The QuantizedLinear-like objects of a layer: anything exposing W_latent,
+    sign_l, sign_r and codebook_gpu (the layer itself, its .modules(), or an
+    iterable of them)."""
+    attrs = ("W_latent", "sign_l", "sign_r", "codebook_gpu")
+    if all(hasattr(layer, a) for a in attrs):
+        return [layer]
+    items = layer.modules() if hasattr(layer, "modules") else layer
+    return [m for m in items if all(hasattr(m, a) for a in attrs)]
+
+
+def measure_ptq_residual(qat_layer):
+    """Mean squared unit-scale residual ||W~/s - RHT(W_q)/s||^2 over every
+    quantized linear of a layer (src/bcjr/anneal.py:110-140): the natural T_0 of
+    the annealing schedule."""
+    accum, count = 0.0, 0
+    for ql in _quantized_linears(qat_layer):
+        ssq, n = ptq_residual(ql.W_latent, ql.sign_l, ql.sign_r, ql.codebook_gpu)
+        accum += ssq
+        count += n
+    return accum / max(count, 1)
+
+
 __all__ = ["quantize_forward_gpu_no_rht", "quantize_forward_gpu", "quantize_forward_numpy", "TrellisQuantSTE",
-           "TrellisQuantSTE_IP", "replay_walks", "ptq_residual"]
+           "TrellisQuantSTE_IP", "replay_walks", "ptq_residual", "measure_ptq_residual"]

@@ -135,3 +135,48 @@ def test_moe_dict_form(bcjr_mod):
     for nm in names:
         ref = bcjr_mod.bcjr_quantize_weight(W[nm], signs[nm][0], signs[nm][1], cb, 0.1, L=16, k=2, V=1)
         assert (out[nm] - ref).abs().max() <= SOFT_TOL * ref.abs().max()
+
+
+def test_ste_experts_bit_exact_vs_oracle(bcjr_mod, oracle):
+    """Hard quantization of several weights in one Viterbi launch: every weight
+    against RHT -> its RMS scale -> tiles -> Viterbi -> untile -> inverse RHT on
+    the oracle, bit for bit (the scale is the same float32 reduction, read back)."""
+    from bcjr.quant import tile_for_viterbi, untile_from_viterbi
+    _say("STE experts vs oracle, HYB L=16")
+    lut = np.random.default_rng(2).standard_normal((512, 2)).astype(np.float32)
+    cb = bcjr_mod.make_hyb_codebook_gpu(lut, 9, 16, "cuda")
+    shapes = [(64, 256), (256, 64), (64, 256)]
+    Ws, SL, SR = _weights(shapes, 41)
+    Wd = [torch.tensor(W, device="cuda") for W in Ws]
+    sl = [torch.tensor(s, device="cuda") for s in SL]
+    sr = [torch.tensor(s, device="cuda") for s in SR]
+    outs = bcjr_mod.ste_quantize_experts(Wd, sl, sr, cb)
+    cb_np = cb.cpu().numpy()
+    for e, (W, a, b) in enumerate(zip(Ws, SL, SR)):
+        m, n = W.shape
+        Wt = bcjr_mod.apply_rht_batched(Wd[e][None], sl[e][None], sr[e][None])
+        s = float(Wt.pow(2).mean(dim=(1, 2)).sqrt()[0])
+        Wt_np = oracle.rht(W, a, b)
+        assert np.array_equal(Wt[0].cpu().numpy(), Wt_np)
+        seqs, info = tile_for_viterbi(torch.tensor(Wt_np / np.float32(s)), 16, 16)
+        _, _, _, recon, _ = oracle.viterbi(seqs.numpy().reshape(seqs.shape[0], -1, 2), cb_np, 16, 4)
+        q = untile_from_viterbi(torch.tensor(recon.reshape(seqs.shape[0], -1)), info, (m, n), 16, 16).numpy()
+        ref = oracle.inverse_rht((q * np.float32(s)).astype(np.float32), a, b)
+        assert np.array_equal(outs[e].cpu().numpy(), ref), e
+
+
+def test_measure_ptq_residual_over_a_layer(bcjr_mod):
+    from types import SimpleNamespace
+    _say("measure_ptq_residual")
+    cb = bcjr_mod.make_3inst_codebook(16, "cuda")
+    qls = [SimpleNamespace(W_latent=torch.randn(m, n, device="cuda") * 0.02,
+                           sign_l=torch.tensor(_signs(m, i), device="cuda"),
+                           sign_r=torch.tensor(_signs(n, 10 + i), device="cuda"), codebook_gpu=cb)
+           for i, (m, n) in enumerate([(64, 64), (128, 64)])]
+    tot, cnt = 0.0, 0
+    for ql in qls:
+        ssq, c = bcjr_mod.ptq_residual(ql.W_latent, ql.sign_l, ql.sign_r, cb)
+        tot, cnt = tot + ssq, cnt + c
+    assert bcjr_mod.measure_ptq_residual(qls) == tot / cnt
+    assert bcjr_mod.measure_ptq_residual(qls[0]) == bcjr_mod.ptq_residual(qls[0].W_latent, qls[0].sign_l,
+                                                                         qls[0].sign_r, cb)[0] / (64 * 64)
