@@ -1,8 +1,8 @@
 """CPU oracle for the BCJR forward-backward path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
-leg may import this package, and only as the checker (or the timed CPU
-baseline).  The product path under ``quant-2bit_amd/`` never imports it.
+leg may import this package, and only to check results against (or as the
+timed CPU baseline).  The product path under ``quant-2bit_amd/`` never imports it.
 
 Contents
 --------

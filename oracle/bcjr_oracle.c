@@ -2,7 +2,7 @@
  * CPU oracle for the BCJR forward-backward path -- TEST INFRASTRUCTURE ONLY.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
- * this library, and only as the checker (or as the timed CPU baseline).  The
+ * this library, and only to check results against (or as the timed CPU baseline).  The
  * product path (quant-2bit_amd/) never links or calls it.
  *
  * It restates, in plain C, the algorithm of the reference's eager BCJR node and

@@ -140,8 +140,8 @@ int grid_for(long long items, int max_blocks) {
 
 // ---------------------------------------------------------------------------
 // Tiled FWHT for n >= 64: a tile of up to 2^15 floats in LDS, stages done in
-// registers a few at a time ("rounds": each thread loads the E
-// elements whose indices differ only in the round's bits, applies those stages
+// registers a few at a time ("radix steps": each thread loads the E
+// elements whose indices differ only in the step's bits, applies those stages
 // in order, and stores them back).  Stage h acts on index bit log2(h) of the
 // tile, so with rows laid out contiguously the row transform is the stages on
 // bits [0, log2 n) and the column transform within the tile is the stages on
@@ -149,15 +149,15 @@ int grid_for(long long items, int max_blocks) {
 // same order, so results are bit-identical to the per-stage kernels.
 //
 //   pass 1 (tile_rows_kernel): RB = 2^14 / n consecutive rows of a matrix (64
-//     KiB, two workgroups per CU); round 0 (bits 0-4) loads 32 consecutive
-//     floats per thread from HBM, later rounds (radix 8) go through LDS, the
+//     KiB, two workgroups per CU); radix step 0 (bits 0-4) loads 32
+//     consecutive floats per thread from HBM, later steps (radix 8) go through LDS, the
 //     last one stores to HBM; the column stages h < RB run on the same tile.
 //   pass 2 (tile_cols_kernel): column stages h0 <= h < h0 * len on tiles of
 //     len <= 1024 rows spaced h0 apart x 32 columns; loads and stores go
 //     straight to HBM (32 lanes = 128 contiguous bytes of a row).
 // An 8192 x 2048 matrix takes 2 passes over HBM (the per-stage kernels take 3).
-// LDS rows of 32 floats carry 4 floats of padding, so round 0's per-thread
-// 32-float runs (128-bit reads) and the later rounds' strided accesses are
+// LDS rows of 32 floats carry 4 floats of padding, so radix step 0's
+// per-thread 32-float runs (128-bit reads) and the later steps' strided accesses are
 // free of bank conflicts.
 // ---------------------------------------------------------------------------
 // pass 1: 2^14-float tiles (72 KiB padded), 512 threads, two workgroups per CU
@@ -192,11 +192,11 @@ __device__ __forceinline__ void slot_stages(float (&v)[E]) {
   }
 }
 
-// One radix-E round on bits [k0, k0 + log2 E) of a tile of T floats: group g
+// One radix-E step on bits [k0, k0 + log2 E) of a tile of T floats: group g
 // holds the E indices base + s * 2^k0.  LD(g, base, v) fills v, ST(g, base, v)
 // stores it; each is written for one address space.
 template <int E, typename LD, typename ST>
-__device__ __forceinline__ void tile_round(uint32_t T, uint32_t k0, LD ld, ST st) {
+__device__ __forceinline__ void radix_step(uint32_t T, uint32_t k0, LD ld, ST st) {
   constexpr uint32_t LE = E == 2 ? 1 : E == 4 ? 2 : 3;
   static_assert(E == 2 || E == 4 || E == 8, "radix");
   const uint32_t lowmask = (1u << k0) - 1u;
@@ -210,7 +210,7 @@ __device__ __forceinline__ void tile_round(uint32_t T, uint32_t k0, LD ld, ST st
 }
 
 template <int E>
-struct LdsIO {  // LDS loads / stores of a round's E elements
+struct LdsIO {  // LDS loads / stores of a radix step's E elements
   float* t;
   uint32_t k0;
   __device__ __forceinline__ void load(uint32_t base, float (&v)[E]) const {
@@ -223,7 +223,7 @@ struct LdsIO {  // LDS loads / stores of a round's E elements
   }
 };
 
-// Round dispatch on the radix (3, 2 or 1 bits).  F(std::integral_constant<int, E>) runs the round.
+// Dispatch on the radix (3, 2 or 1 bits).  F(std::integral_constant<int, E>) runs the step.
 template <typename F>
 __device__ __forceinline__ void with_radix(uint32_t bits, F f) {
   if (bits == 3) f(std::integral_constant<int, 8>());
@@ -259,9 +259,9 @@ __global__ __launch_bounds__(kRowThreads2) void tile_rows_kernel(TileRowsParams 
   float* f_end = f_mid + rb;                         // rb row factors (times scale) at the store
   const uint32_t tiles_per_mat = (uint32_t)P.m / rb;
   const long long tiles = (long long)P.batch * tiles_per_mat;
-  // Rounds: bits [0, 5) from HBM, then 3-bit chunks up to nb (row stages), then
-  // 3-bit chunks up to cb_end (column stages); n >= 64, so at least one round
-  // follows round 0, and the last one stores to HBM.
+  // Radix steps: bits [0, 5) from HBM, then 3-bit chunks up to nb (row stages), then
+  // 3-bit chunks up to cb_end (column stages); n >= 64, so at least one step
+  // follows step 0, and the last one stores to HBM.
   uint32_t last_k0 = 5;
   for (uint32_t k = 5; k < nb; k += 3) last_k0 = k;
   for (uint32_t k = nb; k < cb_end; k += 3) last_k0 = k;
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kRowThreads2) void tile_rows_kernel(TileRowsParams 
       f_mid[i] = P.row_mid ? P.row_mid[(size_t)e * P.m + r0 + i] : 1.0f;
       f_end[i] = (P.row_end ? P.row_end[(size_t)e * P.m + r0 + i] : 1.0f) * P.scale;
     }
-    // round 0: bits [0, 5) from HBM, 32 consecutive floats per thread
+    // radix step 0: bits [0, 5) from HBM, 32 consecutive floats per thread
     for (uint32_t g = threadIdx.x; g < T / 32; g += blockDim.x) {
       float v[32];
       const float4* s4 = reinterpret_cast<const float4*>(src + g * 32);
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(kRowThreads2) void tile_rows_kernel(TileRowsParams 
       for (int j = 0; j < 8; ++j) d4[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
     }
     __syncthreads();
-    // row rounds: bits [5, nb)
+    // row steps: bits [5, nb)
     for (uint32_t k0 = 5; k0 < nb; k0 += 3) {
       const uint32_t bits = nb - k0 < 3 ? nb - k0 : 3;
       with_radix(bits, [&](auto ec) {
@@ -308,9 +308,9 @@ __global__ __launch_bounds__(kRowThreads2) void tile_rows_kernel(TileRowsParams 
         const LdsIO<E> io{t, k0};
         auto ld = [&](uint32_t b, float (&v)[E]) { io.load(b, v); };
         if (k0 != last_k0) {
-          tile_round<E>(T, k0, ld, [&](uint32_t b, const float (&v)[E]) { io.store(b, v); });
+          radix_step<E>(T, k0, ld, [&](uint32_t b, const float (&v)[E]) { io.store(b, v); });
         } else {  // rows only: every factor at the store (columns vary within a group)
-          tile_round<E>(T, k0, ld, [&](uint32_t b, const float (&v)[E]) {
+          radix_step<E>(T, k0, ld, [&](uint32_t b, const float (&v)[E]) {
 #pragma unroll
             for (int s = 0; s < E; ++s) {
               const uint32_t i = b + ((uint32_t)s << k0);
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(kRowThreads2) void tile_rows_kernel(TileRowsParams 
       });
       __syncthreads();
     }
-    // column rounds: bits [nb, cb_end); the group's column is fixed (bits < nb of base)
+    // column steps: bits [nb, cb_end); the group's column is fixed (bits < nb of base)
     for (uint32_t k0 = nb; k0 < cb_end; k0 += 3) {
       const uint32_t bits = cb_end - k0 < 3 ? cb_end - k0 : 3;
       with_radix(bits, [&](auto ec) {
@@ -345,10 +345,10 @@ __global__ __launch_bounds__(kRowThreads2) void tile_rows_kernel(TileRowsParams 
           }
         };
         const bool first = k0 == nb, last = k0 == last_k0;
-        if (first && last) tile_round<E>(T, k0, ld_first, st_hbm);
-        else if (first) tile_round<E>(T, k0, ld_first, st_lds);
-        else if (last) tile_round<E>(T, k0, ld, st_hbm);
-        else tile_round<E>(T, k0, ld, st_lds);
+        if (first && last) radix_step<E>(T, k0, ld_first, st_hbm);
+        else if (first) radix_step<E>(T, k0, ld_first, st_lds);
+        else if (last) radix_step<E>(T, k0, ld, st_hbm);
+        else radix_step<E>(T, k0, ld, st_lds);
       });
       __syncthreads();
     }
@@ -409,10 +409,10 @@ __global__ __launch_bounds__(kColThreads2) void tile_cols_kernel(TileColsParams 
         auto ld = [&](uint32_t b, float (&v)[E]) { io.load(b, v); };
         auto st = [&](uint32_t b, const float (&v)[E]) { io.store(b, v); };
         const bool first = k0 == CB, last = k0 == last_k0;
-        if (first && last) tile_round<E>(T, k0, ld_hbm, st_hbm);
-        else if (first) tile_round<E>(T, k0, ld_hbm, st);
-        else if (last) tile_round<E>(T, k0, ld, st_hbm);
-        else tile_round<E>(T, k0, ld, st);
+        if (first && last) radix_step<E>(T, k0, ld_hbm, st_hbm);
+        else if (first) radix_step<E>(T, k0, ld_hbm, st);
+        else if (last) radix_step<E>(T, k0, ld, st_hbm);
+        else radix_step<E>(T, k0, ld, st);
       });
       __syncthreads();
     }
