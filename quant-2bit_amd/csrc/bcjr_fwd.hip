@@ -57,8 +57,8 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   float* wmax = mbuf + 2 * NT;                                    // 2*kMaxWaves
   float* wsum = wmax + 2 * kMaxWaves;                             // kMaxWaves
   float* wbuf = wsum + kMaxWaves;                                 // N*V   sequence
-  float* spart = wbuf + N * V;                                    // N*nwaves*V per-wave soft partials
-  float* lut = spart + N * nwaves * V;                            // HYB LUT
+  float* spart = wbuf + N * V;                                    // 2*nwaves*V per-wave soft partials
+  float* lut = spart + 2 * nwaves * V;                            // HYB LUT
 
   if constexpr (CODE == CODE_HYB) {
     const int nl = 2 << P.Q;
@@ -90,6 +90,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
     const float sk = sqrtf(kLog2e / Tb);
     const float ssk = CT::kSigma * sk;  // d = (c - w) * sk = h * ssk - w * sk
     const float* seqb = P.seq + (size_t)b * N * V;
+    float* softb = P.soft + (size_t)b * N * V;
     for (int i = tid; i < N * V; i += nthr) wbuf[i] = seqb[i];
     // m~_{-1} = log2(R) everywhere: the buffer step 0 reads from.
     for (int j = tid; j < NT; j += nthr) mbuf[NT + j] = (float)KV;
@@ -264,6 +265,12 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
         if (t != N - 1) {
           Qv = -INFINITY;
           Qv = block_max(wmax + ((k + 1) & 1) * kMaxWaves);
+          // soft of step t+1 from its per-wave partials (the other parity buffer)
+          if (tid < V) {
+            float sacc = 0.0f;
+            for (int w = 0; w < nwaves; ++w) sacc += spart[(((k + 1) & 1) * nwaves + w) * V + tid];
+            softb[(t + 1) * V + tid] = sacc;
+          }
         }
         const float Kt = (float)(cvec[t] + D - logZ2);
         float nw[V];
@@ -417,7 +424,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           const float s = wave_sum(acc[v]);
-          if (lane == 0) spart[(t * nwaves + wave) * V + v] = s * CT::kSigma;
+          if (lane == 0) spart[((k & 1) * nwaves + wave) * V + v] = s * CT::kSigma;
         }
         tmax = wave_max(tmax);
         if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
@@ -430,12 +437,12 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
       sweeps(std::false_type{});
     }
 
-    float* softb = P.soft + (size_t)b * N * V;
-    for (int i = tid; i < N * V; i += nthr) {
-      const int t = i / V, v = i - t * V;
-      float s = 0.0f;
-      for (int w = 0; w < nwaves; ++w) s += spart[(t * nwaves + w) * V + v];
-      softb[i] = s;
+    // soft of step 0: its partials sit in the buffer of the last beta step's parity
+    if (tid < V) {
+      const int par = (2 * N - 1) & 1;  // k after N alpha and N beta steps, minus one
+      float sacc = 0.0f;
+      for (int w = 0; w < nwaves; ++w) sacc += spart[(par * nwaves + w) * V + tid];
+      softb[tid] = sacc;
     }
     if (tid == 0 && P.logZ) P.logZ[b] = (float)(logZ2 * kLn2);
     __syncthreads();
