@@ -70,8 +70,8 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
   float* wsum = wmax + 2 * kMaxWaves;                               // 2*kMaxWaves
   float* wbuf = wsum + 2 * kMaxWaves;                               // N*V
   float* gbuf = wbuf + N * V;                                       // N*V
-  float* apart = gbuf + N * V;                                      // N*nwaves*(V+1)
-  float* lut = apart + N * nwaves * (V + 1);
+  float* apart = gbuf + N * V;                                      // 2*nwaves*(V+1) per-wave partials
+  float* lut = apart + 2 * nwaves * (V + 1);
 
   if constexpr (CODE == CODE_HYB) {
     const int nl = 2 << P.Q;
@@ -120,6 +120,18 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
     const float gZ = P.g_logZ ? P.g_logZ[b] : 0.0f;
     const float* seqb = P.seq + (size_t)b * N * V;
     const float* gb = P.g_soft + (size_t)b * N * V;
+    float* gout = P.g_seq + (size_t)b * N * V;
+    const float twoT = 2.0f / Tb;
+    // d seq_t[v] from the per-wave sums of step t in partial buffer `par`, summed
+    // in wave order
+    auto grad_out = [&](int t, int par, int v) {
+      float a0 = 0.0f, a1 = 0.0f;
+      for (int w = 0; w < nwaves; ++w) {
+        a0 += apart[(par * nwaves + w) * (V + 1)];
+        a1 += apart[(par * nwaves + w) * (V + 1) + 1 + v];
+      }
+      gout[t * V + v] = twoT * (a1 - wbuf[t * V + v] * a0);
+    };
     for (int i = tid; i < N * V; i += nthr) {
       wbuf[i] = seqb[i];
       gbuf[i] = gb[i];
@@ -349,6 +361,8 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
         if (t != N - 1) {
           Qv = -INFINITY;
           Qv = block_max(wmax + ((k + 1) & 1) * kMaxWaves);
+          // gradient of step t+1 from its per-wave partials (the other parity buffer)
+          if (tid < V) grad_out(t + 1, (k + 1) & 1, tid);
         }
         const float Kt = (float)(cvec[t] + D - logZ2);
         float nw[V], sg[V];
@@ -539,11 +553,11 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
         }
         D += (double)Qv;
         A0 = wave_sum(A0);
-        if (lane == 0) apart[(t * nwaves + wave) * (V + 1)] = A0;
+        if (lane == 0) apart[((k & 1) * nwaves + wave) * (V + 1)] = A0;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           const float s = wave_sum(A1[v]);
-          if (lane == 0) apart[(t * nwaves + wave) * (V + 1) + 1 + v] = s * CT::kSigma;
+          if (lane == 0) apart[((k & 1) * nwaves + wave) * (V + 1) + 1 + v] = s * CT::kSigma;
         }
         tmax = wave_max(tmax);
         if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
@@ -557,17 +571,8 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
       sweeps(std::false_type{});
     }
 
-    const float twoT = 2.0f / Tb;
-    float* gout = P.g_seq + (size_t)b * N * V;
-    for (int i = tid; i < N * V; i += nthr) {
-      const int t = i / V, v = i - t * V;
-      float a0 = 0.0f, a1 = 0.0f;
-      for (int w = 0; w < nwaves; ++w) {
-        a0 += apart[(t * nwaves + w) * (V + 1)];
-        a1 += apart[(t * nwaves + w) * (V + 1) + 1 + v];
-      }
-      gout[i] = twoT * (a1 - wbuf[i] * a0);
-    }
+    // step 0's partials sit in the buffer of the last beta step's parity ((2N - 1) & 1)
+    if (tid < V) grad_out(0, 1, tid);
     __syncthreads();
   }
 }

@@ -63,7 +63,7 @@ inline size_t fwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, i
 inline size_t bwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {
   const size_t NT = (size_t)1 << (L - KV);
   size_t b = 8u * (size_t)((N + 1) & ~1);
-  b += 4u * (2 * NT + 4 * 16 + 2 * (size_t)N * V + (size_t)N * nwaves * (V + 1));
+  b += 4u * (2 * NT + 4 * 16 + 2 * (size_t)N * V + 2 * (size_t)nwaves * (V + 1));
   if (code == 3) b += 4u * ((size_t)2 << Q);
   return b;
 }

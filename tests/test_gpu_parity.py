@@ -102,6 +102,7 @@ CASES = [
     (16, 2, 1, 96, 2, "1mad", 0.05),
     (16, 2, 1, 128, 2, "3inst", 0.01),   # the float32 floor the reference states (T >= 1e-2)
     (16, 2, 2, 64, 2, "hyb", 0.1),       # reference QAT trellis (L=16, kV=4)
+    (16, 2, 1, 1024, 1, "3inst", 0.1),   # long sequence: per-step partials are double-buffered
 ]
 
 
