@@ -203,6 +203,16 @@ def main():
         t_f.append(e[0].elapsed_time(e[1]) / 1e3)
         t_b.append(e[2].elapsed_time(e[3]) / 1e3)
     fwd_s, bwd_s = sum(t_f) / reps, sum(t_b) / reps
+    # The forward with the fused marginal entropy (entropy_diagnostic over every tile).
+    t_h = []
+    for _ in range(reps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        e[0].record(stream)
+        ops.forward_entropy(spec, x, args.T, None)
+        e[1].record(stream)
+        torch.cuda.synchronize(dev)
+        t_h.append(e[0].elapsed_time(e[1]) / 1e3)
+    ent_s = sum(t_h) / reps
 
     peaks = measure_peaks(torch, dev)
     exp_peak = peaks["exp"]["per_s"]
@@ -226,6 +236,7 @@ def main():
                             "frac": soft_pc * cells / fwd_s / exp_peak},
         "bcjr_bwd_kernel": {"ms": bwd_s * 1e3, "trans_per_cell": grad_pc,
                             "frac": grad_pc * cells / bwd_s / exp_peak},
+        "bcjr_fwd_kernel (marginal entropy)": {"ms": ent_s * 1e3, "vs_forward": ent_s / fwd_s},
     }
     layer = None
     if args.config == "tile" and not args.no_layer:

@@ -110,6 +110,16 @@ int bcjr_forward_internals(const bcjr_problem* prob, const float* seq, const flo
                            float* marginals, float* log_alpha, float* log_beta,
                            void* ws, size_t ws_bytes, hipStream_t stream);
 
+/* bcjr_forward plus the marginal entropy of every step, entropy (B, N) float32,
+ * H_t = -sum_s P_t(s) ln P_t(s) in nats, accumulated inside the beta sweep: no
+ * (B, N, 2^L) tensor is formed, so it runs on whole layers at about the cost of
+ * bcjr_forward.  Replaces the P-materialising body of entropy_diagnostic
+ * (src/bcjr/anneal.py:143-184, which calls forward_backward.py:190-232 with
+ * return_internals=True and reduces -(P * log P).sum(-1)). */
+int bcjr_forward_entropy(const bcjr_problem* prob, const float* seq, const float* T,
+                         const float* codebook_or_lut, float* soft, float* logZ, float* entropy,
+                         void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* Gradient of sum(g_soft * soft) + sum(g_logZ * logZ) with respect to the
  * sequences, (B, N, V).  g_logZ may be NULL (treated as zero).  logZ is unused
  * (recomputed) and may be NULL.  Codebook and T get no gradient, as in

@@ -9,7 +9,7 @@ Contents
 ``lib()``                 ctypes handle on ``oracle/_build/libbcjr_oracle.so``, the
                           C restatement (``bcjr_oracle.c``) of the reference's
                           eager BCJR node, gradient and Viterbi encoder.
-``codebook / bcjr_forward / bcjr_backward / viterbi / decode``
+``codebook / bcjr_forward / bcjr_backward / marginal_entropy / viterbi / decode``
                           numpy-facing wrappers over the C restatement.
 ``naive_forward``         literal numpy restatement of the reference's eager
                           algorithm (gather over predecessor tables, then
@@ -33,6 +33,8 @@ bcjr_forward / bcjr_backward   brute-force path enumeration on tiny trellises (i
                                checked by finite differences of log Z and soft), the
                                gather form ``naive_forward``, T -> inf / T -> 0 limits,
                                linearity of the gradient in g.
+marginal_entropy               -sum P ln P of naive_forward's P; L ln 2 at T -> inf;
+                               -> 0 at T -> 0 with a unique minimum.
 viterbi / decode               the L=2 known answer of the reference's
                                test_viterbi.py:17-53, brute-force minimum-cost paths,
                                tie rules, the 1MAD Table-1 MSE band, round trips.
@@ -81,7 +83,7 @@ def lib():
         L = ctypes.CDLL(_LIB_PATH)
         i32, i64, fp = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
         L.oracle_codebook.argtypes = [i32, i32, fp, i32, fp]
-        L.oracle_bcjr_forward.argtypes = [i32, i32, i32, i64, i32, fp, fp, i32, fp, fp, fp, i32]
+        L.oracle_bcjr_forward.argtypes = [i32, i32, i32, i64, i32, fp, fp, i32, fp, fp, fp, fp, i32]
         L.oracle_bcjr_backward.argtypes = [i32, i32, i32, i64, i32, fp, fp, i32, fp, fp, fp, fp, i32]
         L.oracle_viterbi.argtypes = [i32, i32, i32, i64, i32, fp, fp, fp, fp, fp, fp, fp, i32]
         L.oracle_decode.argtypes = [i32, i32, i32, i64, i32, fp, fp, fp, fp, fp]
@@ -137,8 +139,26 @@ def bcjr_forward(seq, cb, T, L, KV, nthreads: int = 0):
     soft = np.empty_like(seq)
     logZ = np.empty((B,), dtype=np.float32)
     _check(lib().oracle_bcjr_forward(L, KV, V, B, N, _ptr(seq), _ptr(Ta), per, _ptr(cb),
-                                      _ptr(soft), _ptr(logZ), nthreads), "forward")
+                                      _ptr(soft), _ptr(logZ), None, nthreads), "forward")
     return soft, logZ
+
+
+def marginal_entropy(seq, cb, T, L, KV, nthreads: int = 0):
+    """H (B,N) float32: -sum_s P_t(s) ln P_t(s) in nats, computed in float64 --
+    the per-(b, t) quantity entropy_diagnostic (src/bcjr/anneal.py:175-179)
+    averages.  Pinned by naive_forward's P on small trellises and by the closed
+    forms H = L ln 2 (uniform marginals at T -> inf) and H -> 0 (T -> 0, unique
+    minimum)."""
+    seq = _f32(seq)
+    cb = _f32(cb)
+    B, N, V = seq.shape
+    Ta, per = _temps(T, B)
+    soft = np.empty_like(seq)
+    logZ = np.empty((B,), dtype=np.float32)
+    H = np.empty((B, N), dtype=np.float32)
+    _check(lib().oracle_bcjr_forward(L, KV, V, B, N, _ptr(seq), _ptr(Ta), per, _ptr(cb),
+                                      _ptr(soft), _ptr(logZ), _ptr(H), nthreads), "forward")
+    return H
 
 
 def bcjr_backward(seq, cb, T, L, KV, g_soft, g_logZ=None, nthreads: int = 0):

@@ -224,9 +224,11 @@ static int work_alloc(work_t* w, const trellis_t* tr, int grad) {
     return ORACLE_OK;
 }
 
-/* One sequence, forward: soft (N x V) and logZ. */
+/* One sequence, forward: soft (N x V), logZ and, when H is non-NULL, the
+ * marginal entropy H_t = -sum_s P_t(s) ln P_t(s) (N) -- what entropy_diagnostic
+ * (src/bcjr/anneal.py:175-179) reduces from P. */
 static void fwd_one(const trellis_t* tr, const float* cb, const float* seq, double T,
-                    float* soft, float* logZ_out, work_t* w) {
+                    float* soft, float* logZ_out, float* H, work_t* w) {
     const int64_t S = tr->S, NT = tr->NT, R = tr->R;
     const int KV = tr->KV, V = tr->V, N = tr->N;
     const double invT = 1.0 / T;
@@ -237,14 +239,17 @@ static void fwd_one(const trellis_t* tr, const float* cb, const float* seq, doub
     for (int t = N - 1; t >= 0; --t) {
         emission(tr, cb, seq + (size_t)t * V, invT, w->ll);
         const double* mprev = t ? w->m_all + (size_t)(t - 1) * NT : NULL;
-        double acc[4] = {0, 0, 0, 0};
+        double acc[4] = {0, 0, 0, 0}, h = 0.0;
         for (int64_t s = 0; s < S; ++s) {
             w->y[s] = w->ll[s] + w->n_cur[s & (NT - 1)];
             double mp = mprev ? mprev[s >> KV] : log((double)R);
-            double P = exp(w->y[s] + mp - logZ);
+            const double lp = w->y[s] + mp - logZ;
+            double P = exp(lp);
             for (int v = 0; v < V; ++v) acc[v] += P * (double)cb[s * V + v];
+            if (P > 0.0) h -= P * lp;
         }
         for (int v = 0; v < V; ++v) soft[(size_t)t * V + v] = (float)acc[v];
+        if (H) H[t] = (float)h;
         for (int64_t u = 0; u < NT; ++u) w->n_nxt[u] = lse_array(w->y + u * R, R);
         double* tmp = w->n_cur; w->n_cur = w->n_nxt; w->n_nxt = tmp;
     }
@@ -321,8 +326,9 @@ static int set_threads(int nthreads) {
 int oracle_num_threads(int nthreads) { return set_threads(nthreads); }
 
 /* seq: (B, N, V); T: per-sequence (t_per_seq) or scalar; cb: (2^L, V). */
+/* H: (B, N) marginal entropies in nats, or NULL. */
 int oracle_bcjr_forward(int L, int KV, int V, int64_t B, int N, const float* seq, const float* T,
-                        int t_per_seq, const float* cb, float* soft, float* logZ, int nthreads) {
+                        int t_per_seq, const float* cb, float* soft, float* logZ, float* H, int nthreads) {
     trellis_t tr;
     if (trellis_init(&tr, L, KV, V, N) || B < 0) return ORACLE_EINVAL;
     set_threads(nthreads);
@@ -338,7 +344,8 @@ int oracle_bcjr_forward(int L, int KV, int V, int64_t B, int N, const float* seq
 #pragma omp for schedule(dynamic, 1)
             for (int64_t b = 0; b < B; ++b) {
                 double Tb = (double)(t_per_seq ? T[b] : T[0]);
-                fwd_one(&tr, cb, seq + (size_t)b * N * V, Tb, soft + (size_t)b * N * V, logZ + b, &w);
+                fwd_one(&tr, cb, seq + (size_t)b * N * V, Tb, soft + (size_t)b * N * V, logZ + b,
+                        H ? H + (size_t)b * N : NULL, &w);
             }
             work_free(&w);
         }

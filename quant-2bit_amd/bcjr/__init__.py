@@ -27,6 +27,7 @@ from .serialize import (  # noqa: F401
     dequant_target, dequant_target_gpu, load_packed, load_quantized, pack_bitstreams, precompute_walk_states,
     save_packed, save_quantized, unpack_bitstreams,
 )
+from .anneal import bcjr_marginal_entropy, cosine_temperature_schedule, entropy_diagnostic  # noqa: F401
 from ._lib import LIB_PATH, load as load_library  # noqa: F401
 
 __version__ = "0.1.0"

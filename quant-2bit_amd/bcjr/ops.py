@@ -125,6 +125,25 @@ def forward_internals(spec: Spec, seq: torch.Tensor, T, table: torch.Tensor | No
         return soft, logZ, P, la, lb
 
 
+def forward_entropy(spec: Spec, seq: torch.Tensor, T, table: torch.Tensor | None):
+    """soft, logZ and the marginal entropy H (B, N) in nats, H_t = -sum_s P log P."""
+    with torch.cuda.device(seq.device):
+        seq = seq.detach().to(torch.float32).contiguous()
+        B, N, V = seq.shape
+        Tt, per = _temperature(T, B, seq.device)
+        soft = torch.empty_like(seq)
+        logZ = torch.empty((B,), dtype=torch.float32, device=seq.device)
+        H = torch.empty((B, N), dtype=torch.float32, device=seq.device)
+        if B == 0:
+            return soft, logZ, H
+        prob = spec.problem(B, N, per)
+        ws = _workspace(prob, OP_FORWARD, seq.device)
+        _lib.check(_lib.load().bcjr_forward_entropy(
+            ctypes.byref(prob), _lib.ptr(seq), _lib.ptr(Tt), _lib.ptr(table), _lib.ptr(soft),
+            _lib.ptr(logZ), _lib.ptr(H), _lib.ptr(ws), ws.numel(), _stream(seq.device)), "bcjr_forward_entropy")
+        return soft, logZ, H
+
+
 def backward(spec: Spec, seq: torch.Tensor, T, table, g_soft, g_logZ=None):
     """d seq (B,N,V) float32 of sum(g_soft*soft) + sum(g_logZ*logZ)."""
     with torch.cuda.device(seq.device):

@@ -414,6 +414,33 @@ int bcjr_forward_internals(const bcjr_problem* prob, const float* seq, const flo
   return launch(pl, prob->B, ws_bytes, &P, stream);
 }
 
+int bcjr_forward_entropy(const bcjr_problem* prob, const float* seq, const float* T,
+                         const float* codebook_or_lut, float* soft, float* logZ, float* entropy, void* ws,
+                         size_t ws_bytes, hipStream_t stream) {
+  Plan pl;
+  int rc = make_plan(prob, OP_FWD_INTERNALS, &pl);
+  if (rc) return rc;
+  if (prob->B == 0) return BCJR_OK;
+  if (!seq || !T || !soft || !ws || !entropy)
+    return fail(BCJR_EINVAL, "seq, T, soft, ws and entropy must be non-NULL");
+  if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
+    return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  bcjr::FwdParams P = {};
+  P.seq = seq;
+  P.T = T;
+  P.table = codebook_or_lut;
+  P.soft = soft;
+  P.logZ = logZ;
+  P.ws = static_cast<float*>(ws);
+  P.H_out = entropy;
+  P.B = prob->B;
+  P.N = (int)prob->N;
+  P.L = prob->L;
+  P.Q = prob->Q;
+  P.t_per_seq = prob->t_per_seq ? 1 : 0;
+  return launch(pl, prob->B, ws_bytes, &P, stream);
+}
+
 int bcjr_backward(const bcjr_problem* prob, const float* seq, const float* T, const float* codebook_or_lut,
                   const float* logZ, const float* g_soft, const float* g_logZ, float* g_seq, void* ws,
                   size_t ws_bytes, hipStream_t stream) {

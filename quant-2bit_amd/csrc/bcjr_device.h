@@ -282,6 +282,7 @@ struct FwdParams {
   float* P_out;        // (B, N, S) marginals, or null (diagnostics)
   float* la_out;       // (B, N, S) log alpha (natural log), or null
   float* lb_out;       // (B, N, S) log beta (natural log), or null
+  float* H_out;        // (B, N) marginal entropy in nats, or null (diagnostics)
   long long B;
   int N, L, Q, t_per_seq;
 };

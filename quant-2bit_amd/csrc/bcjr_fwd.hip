@@ -57,8 +57,11 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   float* wmax = mbuf + 2 * NT;                                    // 2*kMaxWaves
   float* wsum = wmax + 2 * kMaxWaves;                             // kMaxWaves
   float* wbuf = wsum + kMaxWaves;                                 // N*V   sequence
-  float* spart = wbuf + N * V;                                    // 2*nwaves*V per-wave soft partials
-  float* lut = spart + 2 * nwaves * V;                            // HYB LUT
+  // Per-wave partials of the step's soft codeword (V values) and, in the
+  // diagnostics variant, of sum_s P log2 P (one more), double-buffered by step.
+  constexpr int SP = V + 1;
+  float* spart = wbuf + N * V;                                    // 2*nwaves*SP per-wave partials
+  float* lut = spart + 2 * nwaves * SP;                           // HYB LUT
 
   if constexpr (CODE == CODE_HYB) {
     const int nl = 2 << P.Q;
@@ -91,6 +94,13 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
     const float ssk = CT::kSigma * sk;  // d = (c - w) * sk = h * ssk - w * sk
     const float* seqb = P.seq + (size_t)b * N * V;
     float* softb = P.soft + (size_t)b * N * V;
+    // Marginal entropy of step t in nats, -ln 2 * sum_s P log2 P, from the
+    // per-wave sums in partial buffer `par`, summed in wave order.
+    auto entropy_out = [&](int t, int par) {
+      float h = 0.0f;
+      for (int w = 0; w < nwaves; ++w) h += spart[(par * nwaves + w) * SP + V];
+      P.H_out[(size_t)b * N + t] = -h * (float)kLn2;
+    };
     for (int i = tid; i < N * V; i += nthr) wbuf[i] = seqb[i];
     // m~_{-1} = log2(R) everywhere: the buffer step 0 reads from.
     for (int j = tid; j < NT; j += nthr) mbuf[NT + j] = (float)KV;
@@ -268,9 +278,10 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
           // soft of step t+1 from its per-wave partials (the other parity buffer)
           if (tid < V) {
             float sacc = 0.0f;
-            for (int w = 0; w < nwaves; ++w) sacc += spart[(((k + 1) & 1) * nwaves + w) * V + tid];
+            for (int w = 0; w < nwaves; ++w) sacc += spart[(((k + 1) & 1) * nwaves + w) * SP + tid];
             softb[(t + 1) * V + tid] = sacc;
           }
+          if (INTERNALS && tid == V && P.H_out) entropy_out(t + 1, (k + 1) & 1);
         }
         const float Kt = (float)(cvec[t] + D - logZ2);
         float nw[V];
@@ -281,9 +292,10 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
         // (maximum 0): no = n~_{t-1}(p*NB + u) and the soft contribution
         // G * sum_c e_c h_c, with pms = raw m~_{t-1}(p*NB + u) + K_t - sh.
         // n holds the raw inputs and pmr the raw m~ (diagnostics only).
+        // hs = sum over the output's R states of P log2 P (diagnostics variant).
         auto beta_out = [&](auto shift_tag, int i, int p, uint32_t xu, int u, const float (&nr)[R],
                             const float (&n)[R], float pms, float pmr, float oout, float& no,
-                            float (&cs)[V]) -> float {
+                            float (&cs)[V], float& hs) -> float {
           constexpr bool SHIFT = decltype(shift_tag)::value;
           float y[R], hh[R][V];
 #pragma unroll
@@ -321,16 +333,25 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 #pragma unroll
           for (int v = 0; v < V; ++v) cs[v] = G * ec[v];
           no = flog2(s) + (M - oout);
-          if constexpr (INTERNALS) {  // diagnostics (small B): P, log alpha, log beta in nats
-            const float Ct = (float)cvec[t];
-            const float Dt = (float)D;
-            const size_t base = ((size_t)b * N + t) * ((size_t)NT << KV) + (size_t)p * NT + (size_t)R * u;
+          hs = 0.0f;
+          if constexpr (INTERNALS) {  // diagnostics: P, log alpha, log beta in nats; entropy
+            if (P.P_out) {
+              const float Ct = (float)cvec[t];
+              const float Dt = (float)D;
+              const size_t base = ((size_t)b * N + t) * ((size_t)NT << KV) + (size_t)p * NT + (size_t)R * u;
 #pragma unroll
-            for (int c = 0; c < R; ++c) {
-              P.P_out[base + c] = e[c] * G;
-              P.la_out[base + c] = (y[c] - nr[c] + pmr + Ct) * (float)kLn2;
-              P.lb_out[base + c] = (n[c] + Dt) * (float)kLn2;
+              for (int c = 0; c < R; ++c) {
+                P.P_out[base + c] = e[c] * G;
+                P.la_out[base + c] = (y[c] - nr[c] + pmr + Ct) * (float)kLn2;
+                P.lb_out[base + c] = (n[c] + Dt) * (float)kLn2;
+              }
             }
+            // log2 P of state c is y[c] - M + (pms + M) = y[c] + pms, so
+            // sum_c P log2 P = G (sum_c e_c y_c + pms s).
+            float ey = 0.0f;
+#pragma unroll
+            for (int c = 0; c < R; ++c) ey = fmaf(e[c], y[c], ey);
+            hs = G * fmaf(pms, s, ey);
           }
           return s;
         };
@@ -338,7 +359,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
         auto read_in = [&](int i, float (&n)[R]) { load_vec<R>(prev + R * min(tid + i * nthr, NB - 1), n); };
         float nx[R];
         read_in(0, nx);
-        float acc[V];
+        float acc[V], hacc = 0.0f;
 #pragma unroll
         for (int v = 0; v < V; ++v) acc[v] = 0.0f;
         float tmax = -INFINITY;
@@ -373,30 +394,34 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
             const float oout = sh + Qv;
             const float kts = Kt - sh;
             if constexpr (kPair) {
-              float no[R], smin = 0.0f, ua[V];
+              float no[R], smin = 0.0f, ua[V], uh = 0.0f;
 #pragma unroll
               for (int v = 0; v < V; ++v) ua[v] = 0.0f;
 #pragma unroll
               for (int p = 0; p < R; ++p) {
-                float cs[V];
-                const float s = beta_out(Fast{}, i, p, xu, u, nr, n, pm[p] + kts, pm[p], oout, no[p], cs);
+                float cs[V], hs;
+                const float s = beta_out(Fast{}, i, p, xu, u, nr, n, pm[p] + kts, pm[p], oout, no[p], cs, hs);
                 smin = p ? fminf(smin, s) : s;
 #pragma unroll
                 for (int v = 0; v < V; ++v) ua[v] += cs[v];
+                uh += hs;
               }
               if constexpr (!EXACT) {
                 if (smin < kUnderflow) {
+                  uh = 0.0f;
 #pragma unroll
                   for (int v = 0; v < V; ++v) ua[v] = 0.0f;
 #pragma unroll
                   for (int p = 0; p < R; ++p) {
-                    float cs[V];
-                    beta_out(std::true_type{}, i, p, xu, u, nr, n, pm[p] + kts, pm[p], oout, no[p], cs);
+                    float cs[V], hs;
+                    beta_out(std::true_type{}, i, p, xu, u, nr, n, pm[p] + kts, pm[p], oout, no[p], cs, hs);
 #pragma unroll
                     for (int v = 0; v < V; ++v) ua[v] += cs[v];
+                    uh += hs;
                   }
                 }
               }
+              hacc += uh;
 #pragma unroll
               for (int v = 0; v < V; ++v) acc[v] += ua[v];
 #pragma unroll
@@ -408,12 +433,14 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
               const float* src = slot_src(t, i);
 #pragma unroll 1
               for (int p = 0; p < R; ++p) {
-                float no, cs[V];
+                float no, cs[V], hs;
                 const float pmr = src[p];
-                const float s = beta_out(Fast{}, i, p, xu, u, nr, n, pmr + kts, pmr, oout, no, cs);
-                if (!EXACT && s < kUnderflow) beta_out(std::true_type{}, i, p, xu, u, nr, n, pmr + kts, pmr, oout, no, cs);
+                const float s = beta_out(Fast{}, i, p, xu, u, nr, n, pmr + kts, pmr, oout, no, cs, hs);
+                if (!EXACT && s < kUnderflow)
+                  beta_out(std::true_type{}, i, p, xu, u, nr, n, pmr + kts, pmr, oout, no, cs, hs);
 #pragma unroll
                 for (int v = 0; v < V; ++v) acc[v] += cs[v];
+                hacc += hs;
                 cur[p * NB + u] = no;
                 tmax = fmaxf(tmax, no);
               }
@@ -424,7 +451,11 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           const float s = wave_sum(acc[v]);
-          if (lane == 0) spart[((k & 1) * nwaves + wave) * V + v] = s * CT::kSigma;
+          if (lane == 0) spart[((k & 1) * nwaves + wave) * SP + v] = s * CT::kSigma;
+        }
+        if constexpr (INTERNALS) {
+          const float h = wave_sum(hacc);
+          if (lane == 0) spart[((k & 1) * nwaves + wave) * SP + V] = h;
         }
         tmax = wave_max(tmax);
         if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
@@ -438,21 +469,25 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
     }
 
     // soft of step 0: its partials sit in the buffer of the last beta step's parity
+    const int par0 = (2 * N - 1) & 1;  // k after N alpha and N beta steps, minus one
     if (tid < V) {
-      const int par = (2 * N - 1) & 1;  // k after N alpha and N beta steps, minus one
       float sacc = 0.0f;
-      for (int w = 0; w < nwaves; ++w) sacc += spart[(par * nwaves + w) * V + tid];
+      for (int w = 0; w < nwaves; ++w) sacc += spart[(par0 * nwaves + w) * SP + tid];
       softb[tid] = sacc;
     }
+    if (INTERNALS && tid == V && P.H_out) entropy_out(0, par0);
     if (tid == 0 && P.logZ) P.logZ[b] = (float)(logZ2 * kLn2);
     __syncthreads();
   }
 }
 
+// The diagnostics variant carries more live values per butterfly, so it caches
+// codewords within the backward's smaller register budget.
 #define BCJR_FWD_CASE(KV_, V_, CODE_, UPT_)                                                      \
   if (KV == KV_ && V == V_ && code == CODE_ && upt == UPT_) {                                   \
     constexpr int CU_ = fwd_cached_units(KV_, V_, UPT_);                                        \
-    return internals ? reinterpret_cast<const void*>(&bcjr_fwd_kernel<KV_, V_, CODE_, UPT_, CU_, true>) \
+    constexpr int CUD_ = bwd_cached_units(KV_, V_, UPT_);                                       \
+    return internals ? reinterpret_cast<const void*>(&bcjr_fwd_kernel<KV_, V_, CODE_, UPT_, CUD_, true>) \
                      : reinterpret_cast<const void*>(&bcjr_fwd_kernel<KV_, V_, CODE_, UPT_, CU_, false>); \
   }
 

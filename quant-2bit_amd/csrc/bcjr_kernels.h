@@ -55,7 +55,7 @@ hipError_t launch_fwht_tiled(const float* x, float* out, int batch, int m, int n
 inline size_t fwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {
   const size_t NT = (size_t)1 << (L - KV);
   size_t b = 8u * (size_t)((N + 1) & ~1);          // C_t (double), padded to 16 bytes
-  b += 4u * (2 * NT + 3 * 16 + (size_t)N * V + 2 * (size_t)nwaves * V);
+  b += 4u * (2 * NT + 3 * 16 + (size_t)N * V + 2 * (size_t)nwaves * (V + 1));
   if (code == 3) b += 4u * ((size_t)2 << Q);
   return b;
 }

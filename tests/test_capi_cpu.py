@@ -185,3 +185,15 @@ def test_expert_dispatch_validates_before_device():
     with pytest.raises(AssertionError, match="expected 1 or 2"):
         bcjr.bcjr_quantize_experts([torch.zeros(64, 64)] * 2, s, s, None, [0.1, 0.2, 0.3])
     assert bcjr.bcjr_quantize_experts([], [], [], None, 0.1) == []
+
+
+def test_cosine_temperature_schedule():
+    """anneal.py:53-61: T_0 at step 0, T_min from the last step on."""
+    from bcjr import cosine_temperature_schedule as sched
+    assert sched(0, 100, 1.0, 0.01) == 1.0
+    assert abs(sched(99, 100, 1.0, 0.01) - 0.01) < 1e-15
+    assert sched(500, 100, 1.0, 0.01) == sched(99, 100, 1.0, 0.01)
+    assert sched(-3, 100, 1.0, 0.01) == 1.0
+    assert sched(5, 1, 1.0, 0.01) == 0.01
+    mid = sched(50, 101, 2.0, 0.0)  # cos(pi/2) = 0: the midpoint is the mean
+    assert abs(mid - 1.0) < 1e-12

@@ -119,6 +119,44 @@ def test_gradient_linear_in_upstream(oracle):
     assert max_rel(d1 + d2, d12) < 1e-5
 
 
+def _entropy(P):
+    P = np.asarray(P, dtype=np.float64)
+    return -np.where(P > 0, P * np.log(np.where(P > 0, P, 1.0)), 0.0).sum(-1)
+
+
+@pytest.mark.parametrize("L,KV,V,N,T", TINY[:5])
+def test_marginal_entropy_matches_brute_force(oracle, L, KV, V, N, T):
+    """-sum P ln P of the path-enumerated marginals (independent of the recursion)."""
+    rng = np.random.default_rng(40 + L * 100 + N)
+    seq = rng.standard_normal((2, N, V)).astype(np.float32)
+    cb = rng.standard_normal((1 << L, V)).astype(np.float32)
+    H = oracle.marginal_entropy(seq, cb, T, L, KV)
+    assert H.shape == (2, N) and H.dtype == np.float32
+    for b in range(2):
+        bf = oracle.brute_force(seq[b], cb, T, L, KV)
+        assert np.abs(H[b] - _entropy(bf["marg"])).max() < 2e-6 * L
+
+
+def test_marginal_entropy_matches_gather_form(oracle):
+    rng = np.random.default_rng(12)
+    L, KV, V, N, T = 10, 2, 1, 16, 0.2
+    seq = rng.standard_normal((3, N, V)).astype(np.float32)
+    cb = rng.standard_normal((1 << L, V)).astype(np.float32)
+    _, _, P, _, _ = oracle.naive_forward(seq, cb, T, L, KV, return_internals=True)
+    assert np.abs(oracle.marginal_entropy(seq, cb, T, L, KV) - _entropy(P)).max() < 1e-5
+
+
+def test_marginal_entropy_limits(oracle):
+    """T -> inf: every state has the same number of paths, so P_t is uniform and
+    H = L ln 2.  T -> 0 with a unique minimum-cost path: H -> 0."""
+    rng = np.random.default_rng(13)
+    L, KV = 8, 2
+    cb = rng.standard_normal((1 << L, 1)).astype(np.float32)
+    seq = rng.standard_normal((2, 9, 1)).astype(np.float32)
+    assert np.abs(oracle.marginal_entropy(seq, cb, 1e7, L, KV) - L * np.log(2.0)).max() < 1e-5
+    assert oracle.marginal_entropy(seq, cb, 1e-4, L, KV).max() < 1e-3
+
+
 # ------------------------------- Viterbi ---------------------------------
 
 def test_viterbi_toy_known_answer(oracle):
