@@ -101,7 +101,7 @@ __device__ __forceinline__ void codeword(uint32_t s, const float* __restrict__ t
 // s = p*NT + R*u + c this is x = (A*R*u + B) + A*(p*NT + c): one integer add per
 // state on top of a per-butterfly base.  h is exact:
 //   1MAD : h = (byte sum of x) - 510   (v_sad_u8 with the -510 in its accumulator)
-//   3INST: h = f16(lo) + f16(hi)       (one v_dot2 with (1, 1); the sum is exact)
+//   3INST: h = f16(lo) + f16(hi)       (one v_fma_mix_f32; the sum is exact)
 // Tables and HYB have kSigma = 1 and h = c.
 // ---------------------------------------------------------------------------
 template <int CODE> struct CodeTraits {
@@ -117,16 +117,21 @@ template <> struct CodeTraits<CODE_3INST> {
   static constexpr float kSigma = (float)(1.0 / 1.2447);
 };
 
-typedef _Float16 bcjr_half2 __attribute__((ext_vector_type(2)));
-
 template <int CODE>
 __device__ __forceinline__ float raw_from_hash(uint32_t x) {
   if constexpr (CODE == CODE_1MAD) {
     return (float)(int)__builtin_amdgcn_sad_u8(x, 0u, (uint32_t)-510);
   } else {
+    // lo * 1 + hi with f16 sources is one v_fma_mix_f32 (exact: both halves lie
+    // in [2^-3, 2) in magnitude).  The 1.0 sits in an SGPR the optimiser cannot
+    // see through; a literal 1.0 folds to an add of two converts (three
+    // instructions), and v_dot2c needs a zeroed accumulator (two).
     const uint32_t y = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
-    const bcjr_half2 one = {(_Float16)1.0f, (_Float16)1.0f};
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(bcjr_half2, y), one, 0.0f, false);
+    float one = 1.0f;
+    asm("" : "+s"(one));
+    const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(y & 0xFFFFu));
+    const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(y >> 16));
+    return fmaf((float)lo, one, (float)hi);
   }
 }
 
