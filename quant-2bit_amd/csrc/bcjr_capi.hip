@@ -261,9 +261,23 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
     // (fwd_cached_units).
     pl->cache = !fwd && (pl->NSUB == 1) && (upt * R * R * p->V <= 128);
     pl->fn = fwd ? bcjr::fwd_kernel_ptr(KV, p->V, p->code, upt, op == OP_FWD_INTERNALS)
-                 : bcjr::vit_kernel_ptr(KV, p->V, p->code, upt, pl->cache);
+                 : bcjr::vit_kernel_ptr(KV, p->V, p->code, upt, pl->cache, false);
+    if (!fwd && pl->NU >= 1024) {
+      // 1024 threads (four waves per SIMD instead of two) when an instance
+      // exists: codewords cached within 64 VGPRs, or none cached (kV = 4).
+      const int upt_w = pl->NU / 1024;
+      const bool cache_w = (pl->NSUB == 1) && (upt_w * R * R * p->V <= 64);
+      const void* fn_w = bcjr::vit_kernel_ptr(KV, p->V, p->code, upt_w, cache_w, true);
+      if (fn_w) {
+        pl->fn = fn_w;
+        pl->cache = cache_w;
+        pl->nthr = nthr = 1024;
+        pl->upt = upt_w;
+      }
+    }
     pl->lds = fwd ? bcjr::fwd_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q)
-                  : bcjr::vit_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q);
+                  : bcjr::vit_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q,
+                                        !pl->cache && pl->nthr == 1024);
     pl->slot_bytes = fwd ? (size_t)N * pl->NT * sizeof(float) : (size_t)N * pl->NT;
   } else {
     pl->cache = false;

@@ -71,6 +71,20 @@ __device__ __forceinline__ void code_hyb(uint32_t s, const float* lut, int Q, fl
   c1 = (x & 0x8000u) ? -b : b;
 }
 
+// The same codeword from 2^rep interleaved copies of the LUT in LDS: entry e of
+// copy k is the float2 at e * 2^rep + k.  With 16 copies, copy k sits in LDS
+// bank pair k whatever the entry, so a half-wave of lanes each reading copy
+// (lane mod 16) is at most 2-way conflicted instead of the ~5-way of 32 random
+// 8-byte reads of one copy.
+__device__ __forceinline__ void code_hyb_rep(uint32_t s, const float2* lut2, int Q, int rep, uint32_t copy,
+                                             float& c0, float& c1) {
+  const uint32_t x = __umul24(s, s) + s;
+  const uint32_t idx = (x >> (15 - Q)) & ((1u << Q) - 1u);
+  const float2 v = lut2[(idx << rep) | copy];
+  c0 = v.x;
+  c1 = (x & 0x8000u) ? -v.y : v.y;
+}
+
 // c(s) for the soft kernels.  `table` is the global (S, V) codebook for
 // CODE_TABLE; `lut` the LDS copy of the HYB LUT.
 template <int CODE, int V>

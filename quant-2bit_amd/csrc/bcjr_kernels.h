@@ -33,7 +33,7 @@ constexpr int bwd_cached_units(int KV, int V, int upt) {
 
 const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool internals);
 const void* bwd_kernel_ptr(int KV, int V, int code, int upt);
-const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache);
+const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache, bool wide);
 const void* decode_kernel_ptr(int KV, int V, int code);
 const void* dequant_kernel_ptr(int KV, int V, int code, bool vec4);
 const void* dequant_t16_kernel_ptr(int KV, int V, int code, int fmt);
@@ -68,12 +68,19 @@ inline size_t bwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, i
   return b;
 }
 
-inline size_t vit_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {
+// log2 of the HYB LUT copies the kV = 4 Viterbi keeps: 16, or as many as fit
+// 64 KiB (2^Q entries of 8 bytes).
+__host__ __device__ constexpr int hyb_lut_rep(int Q) { return 13 - Q < 4 ? 13 - Q : 4; }
+
+// rep_lut: a HYB LUT is staged as 2^hyb_lut_rep(Q) interleaved copies (the
+// uncached 1024-thread instances), else as one.
+inline size_t vit_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q, bool rep_lut) {
   const size_t NT = (size_t)1 << (L - KV);
   (void)nwaves;
   size_t b = 8u * 16;                                           // per-wave MSE partials
   b += 4u * (2 * NT + (size_t)N * V + 2 * 16 + (size_t)N);      // state, seq, argmin, walk
-  if (code == 3) b += 4u * ((size_t)2 << Q);
+  b = (b + 15) & ~(size_t)15;
+  if (code == 3) b += 8u * ((size_t)1 << Q << (rep_lut ? hyb_lut_rep(Q) : 0));
   return b;
 }
 

@@ -26,8 +26,11 @@ __device__ __forceinline__ bool vi_less(float a, int ia, float b, int ib) {
   return (a < b) || (a == b && ia < ib);
 }
 
-template <int KV, int V, int CODE, int UPT, bool CACHE>
-__global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
+// MAXT is the largest workgroup the instance is built for: 1024 threads (four
+// waves per SIMD, at most 128 VGPRs) where the codeword cache fits that budget,
+// else 512.
+template <int KV, int V, int CODE, int UPT, bool CACHE, int MAXT>
+__global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
   constexpr int R = 1 << KV;
   constexpr int RO = R < 4 ? R : 4;
   constexpr int NSUB = R / RO;
@@ -51,11 +54,29 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
   float* redv = wbuf + N * V;                                  // kMaxWaves
   int* redi = reinterpret_cast<int*>(redv + kMaxWaves);        // kMaxWaves
   int* walkbuf = redi + kMaxWaves;                             // N
-  float* lut = reinterpret_cast<float*>(walkbuf + N);
+  // HYB LUT (16-byte aligned): the uncached 1024-thread instances (kV = 4),
+  // which gather an entry per state and step, keep 2^rep interleaved copies read
+  // at copy (lane mod 2^rep) (code_hyb_rep); the others one copy.
+  const size_t lut_off = ((size_t)(reinterpret_cast<unsigned char*>(walkbuf + N) - smem) + 15) & ~(size_t)15;
+  float2* lut2 = reinterpret_cast<float2*>(smem + lut_off);
+  const float* lut = reinterpret_cast<const float*>(lut2);
+  const int rep = (!CACHE && MAXT == 1024) ? hyb_lut_rep(P.Q) : 0;
+  const uint32_t copy = (uint32_t)lane & ((1u << rep) - 1u);
+  // c(s) for the state loops: HYB through the copies, other codes as codeword().
+  auto cword = [&](uint32_t s, float (&c)[V]) {
+    if constexpr (CODE == CODE_HYB) {
+      code_hyb_rep(s, lut2, P.Q, rep, copy, c[0], c[1]);
+    } else {
+      codeword<CODE, V>(s, P.table, lut, P.Q, c);
+    }
+  };
 
   if constexpr (CODE == CODE_HYB) {
-    const int nl = 2 << P.Q;
-    for (int i = tid; i < nl; i += nthr) lut[i] = P.table[i];
+    const int nl = (1 << P.Q) << rep;
+    for (int i = tid; i < nl; i += nthr) {
+      const int e = i >> rep;
+      lut2[i] = make_float2(P.table[2 * e], P.table[2 * e + 1]);
+    }
     __syncthreads();
   }
 
@@ -68,7 +89,7 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
       for (int p = 0; p < R; ++p)
 #pragma unroll
         for (int r = 0; r < R; ++r)
-          codeword<CODE, V>((uint32_t)(p * NT + R * u + r), P.table, lut, P.Q, cw[i][p][r]);
+          cword((uint32_t)(p * NT + R * u + r), cw[i][p][r]);
     }
   }
 
@@ -109,7 +130,7 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
 #pragma unroll
                 for (int v = 0; v < V; ++v) c[v] = cw[i][p][r][v];
               } else {
-                codeword<CODE, V>((uint32_t)(p * NT + R * u + rr), P.table, lut, P.Q, c);
+                cword((uint32_t)(p * NT + R * u + rr), c);
               }
               float e = 0.0f;
 #pragma unroll
@@ -161,7 +182,7 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
       {
         for (int s = tid; s < (NT << KV); s += nthr) {
           float c[V];
-          codeword<CODE, V>((uint32_t)s, P.table, lut, P.Q, c);
+          cword((uint32_t)s, c);
           float e = 0.0f;
 #pragma unroll
           for (int v = 0; v < V; ++v) {
@@ -247,7 +268,7 @@ __global__ __launch_bounds__(512) void bcjr_viterbi_kernel(VitParams P) {
       if (P.walk) P.walk[(size_t)b * N + t] = st;
       if (P.bits) P.bits[(size_t)b * N + t] = st & (R - 1);
       float c[V];
-      codeword<CODE, V>((uint32_t)st, P.table, lut, P.Q, c);
+      cword((uint32_t)st, c);
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         if (P.recon) P.recon[((size_t)b * N + t) * V + v] = c[v];
@@ -576,17 +597,26 @@ __global__ __launch_bounds__(256) void bcjr_codebook_kernel(CbParams P) {
   }
 }
 
-#define BCJR_VIT_CASE(KV_, V_, CODE_, UPT_, CACHE_)                                         \
-  if (KV == KV_ && V == V_ && code == CODE_ && upt == UPT_ && cache == CACHE_)              \
-    return reinterpret_cast<const void*>(&bcjr_viterbi_kernel<KV_, V_, CODE_, UPT_, CACHE_>);
+#define BCJR_VIT_CASE(KV_, V_, CODE_, UPT_, CACHE_)                                              \
+  if (!wide && KV == KV_ && V == V_ && code == CODE_ && upt == UPT_ && cache == CACHE_)          \
+    return reinterpret_cast<const void*>(&bcjr_viterbi_kernel<KV_, V_, CODE_, UPT_, CACHE_, 512>);
+#define BCJR_VIT_WIDE(KV_, V_, CODE_, UPT_, CACHE_)                                              \
+  if (wide && KV == KV_ && V == V_ && code == CODE_ && upt == UPT_ && cache == CACHE_)           \
+    return reinterpret_cast<const void*>(&bcjr_viterbi_kernel<KV_, V_, CODE_, UPT_, CACHE_, 1024>);
 
 #define BCJR_VIT_UPTS(KV_, V_, CODE_, CACHE_) \
   BCJR_VIT_CASE(KV_, V_, CODE_, 1, CACHE_)    \
   BCJR_VIT_CASE(KV_, V_, CODE_, 2, CACHE_)    \
   BCJR_VIT_CASE(KV_, V_, CODE_, 4, CACHE_)    \
   BCJR_VIT_CASE(KV_, V_, CODE_, 8, CACHE_)
+#define BCJR_VIT_WIDE_UPTS(KV_, V_, CODE_) \
+  BCJR_VIT_WIDE(KV_, V_, CODE_, 1, true)   \
+  BCJR_VIT_WIDE(KV_, V_, CODE_, 2, true)   \
+  BCJR_VIT_WIDE(KV_, V_, CODE_, 4, true)
 
-const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache) {
+// wide: the 1024-thread instances, for units >= 1024 (L >= 14 at kV = 2, L = 16
+// at kV = 4) whenever the thread's codewords fit 64 VGPRs or are not cached.
+const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache, bool wide) {
   BCJR_VIT_CASE(1, 1, CODE_TABLE, 1, true)
   BCJR_VIT_UPTS(2, 1, CODE_TABLE, true)
   BCJR_VIT_UPTS(2, 1, CODE_1MAD, true)
@@ -607,6 +637,18 @@ const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache) {
   BCJR_VIT_CASE(4, 2, CODE_TABLE, 2, false)
   BCJR_VIT_CASE(4, 2, CODE_HYB, 1, false)
   BCJR_VIT_CASE(4, 2, CODE_HYB, 2, false)
+  BCJR_VIT_WIDE_UPTS(2, 1, CODE_TABLE)
+  BCJR_VIT_WIDE_UPTS(2, 1, CODE_1MAD)
+  BCJR_VIT_WIDE_UPTS(2, 1, CODE_3INST)
+  BCJR_VIT_WIDE(2, 2, CODE_TABLE, 1, true)
+  BCJR_VIT_WIDE(2, 2, CODE_TABLE, 2, true)
+  BCJR_VIT_WIDE(2, 2, CODE_HYB, 1, true)
+  BCJR_VIT_WIDE(2, 2, CODE_HYB, 2, true)
+  BCJR_VIT_WIDE(4, 1, CODE_TABLE, 1, false)
+  BCJR_VIT_WIDE(4, 1, CODE_1MAD, 1, false)
+  BCJR_VIT_WIDE(4, 1, CODE_3INST, 1, false)
+  BCJR_VIT_WIDE(4, 2, CODE_TABLE, 1, false)
+  BCJR_VIT_WIDE(4, 2, CODE_HYB, 1, false)
   return nullptr;
 }
 

@@ -237,7 +237,9 @@ VIT_CASES = [  # (L, k, V, N, B, kind)
     (10, 1, 2, 64, 4, "hyb"),
     (16, 2, 1, 256, 4, "1mad"),
     (16, 2, 1, 256, 4, "3inst"),
-    (16, 2, 2, 128, 2, "hyb"),
+    (16, 2, 2, 128, 2, "hyb"),         # 1024 threads, 16 interleaved LUT copies
+    (15, 1, 2, 64, 2, "hyb"),          # 1024 threads, cached codewords, 2 butterflies per thread
+    (14, 2, 1, 128, 3, "3inst"),       # 1024 threads, one butterfly per thread
 ]
 
 
