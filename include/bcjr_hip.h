@@ -15,6 +15,8 @@
  *                  (eager autograd of forward_backward.py:106-232)
  *   bcjr_viterbi   src/viterbi/cuda_kernel.py:166-220    viterbi_encode_v_batched_cuda,
  *                  with the tie rules of src/viterbi/encode.py:250-307
+ *   bcjr_viterbi_constrained  src/viterbi/encode.py:105-172, 328-389
+ *                  (viterbi_encode_constrained, _v: the inner pass of tail-biting)
  *   bcjr_decode    src/viterbi/encode.py:310-325 (viterbi_decode_v) and
  *                  src/qat/ste.py:270-283 (_replay_walks)
  *   bcjr_dequant   src/quantize/serialize.py:56-107 (dequant_target, before the
@@ -140,6 +142,19 @@ int bcjr_backward(const bcjr_problem* prob, const float* seq, const float* T,
 int bcjr_viterbi(const bcjr_problem* prob, const float* seq, const float* codebook_or_lut,
                  int32_t* walk, int32_t* bitstream, int32_t* start_state, float* recon,
                  float* mse, uint8_t* packed, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* bcjr_viterbi under the tail-biting constraint of viterbi_encode_constrained_v
+ * (src/viterbi/encode.py:328-389; V = 1: :105-172): with ob = overlap_bits and
+ * v = overlap[b] mod 2^ob, the walk's first state has its top ob bits equal
+ * to v and its last state its bottom ob bits equal to v, cost 1e18 standing in
+ * for an excluded state as in the reference.  0 <= overlap_bits <= L - k*V
+ * (the tail-biting encoder uses L - k*V).  overlap is (B,) int32 on the device.
+ * A sequence with no walk meeting the constraint (the reference raises) gets
+ * start_state = -1; its other outputs are unspecified. */
+int bcjr_viterbi_constrained(const bcjr_problem* prob, const float* seq, const float* codebook_or_lut,
+                             int overlap_bits, const int32_t* overlap, int32_t* walk,
+                             int32_t* bitstream, int32_t* start_state, float* recon, float* mse,
+                             uint8_t* packed, void* ws, size_t ws_bytes, hipStream_t stream);
 
 /* Replay walks: state_t = ((state_{t-1} << kV) | bits_t) & (2^L - 1) from
  * start_state, recon = c(state).  Reads `packed` when non-NULL, else

@@ -9,7 +9,7 @@ Contents
 ``lib()``                 ctypes handle on ``oracle/_build/libbcjr_oracle.so``, the
                           C restatement (``bcjr_oracle.c``) of the reference's
                           eager BCJR node, gradient and Viterbi encoder.
-``codebook / bcjr_forward / bcjr_backward / marginal_entropy / viterbi / decode``
+``codebook / bcjr_forward / bcjr_backward / marginal_entropy / viterbi / viterbi_tailbiting / decode``
                           numpy-facing wrappers over the C restatement.
 ``naive_forward``         literal numpy restatement of the reference's eager
                           algorithm (gather over predecessor tables, then
@@ -37,7 +37,12 @@ marginal_entropy               -sum P ln P of naive_forward's P; L ln 2 at T -> 
                                -> 0 at T -> 0 with a unique minimum.
 viterbi / decode               the L=2 known answer of the reference's
                                test_viterbi.py:17-53, brute-force minimum-cost paths,
-                               tie rules, the 1MAD Table-1 MSE band, round trips.
+                               tie rules, the 1MAD Table-1 MSE band, round trips;
+                               the constrained form against brute force over the
+                               paths that meet the constraint (and its infeasible
+                               cases), overlap_bits = 0 against the unconstrained.
+viterbi_tailbiting             the wrap-around property of every walk and the MSE
+                               gap of the reference's gate (test_viterbi.py:135-197).
 codebook                       golden vectors written from src/codes/ref.py
                                (tests/golden/code_vectors.json).
 pack_bits / unpack_bits        round trips and hand-checked byte layouts.
@@ -85,7 +90,7 @@ def lib():
         L.oracle_codebook.argtypes = [i32, i32, fp, i32, fp]
         L.oracle_bcjr_forward.argtypes = [i32, i32, i32, i64, i32, fp, fp, i32, fp, fp, fp, fp, i32]
         L.oracle_bcjr_backward.argtypes = [i32, i32, i32, i64, i32, fp, fp, i32, fp, fp, fp, fp, i32]
-        L.oracle_viterbi.argtypes = [i32, i32, i32, i64, i32, fp, fp, fp, fp, fp, fp, fp, i32]
+        L.oracle_viterbi.argtypes = [i32, i32, i32, i64, i32, fp, fp, fp, fp, fp, fp, fp, i32, fp, i32]
         L.oracle_decode.argtypes = [i32, i32, i32, i64, i32, fp, fp, fp, fp, fp]
         L.oracle_num_threads.argtypes = [i32]
         for name in ("oracle_codebook", "oracle_bcjr_forward", "oracle_bcjr_backward",
@@ -175,11 +180,14 @@ def bcjr_backward(seq, cb, T, L, KV, g_soft, g_logZ=None, nthreads: int = 0):
     return d
 
 
-def viterbi(seq, cb, L, KV, nthreads: int = 0):
+def viterbi(seq, cb, L, KV, nthreads: int = 0, overlap=None, overlap_bits: int = 0):
     """Direct-form float32 Viterbi (src/viterbi/encode.py:250-307), batched.
 
     seq: (B, N, V).  Returns walk (B,N) int32, bitstream (B,N) int32,
     start_state (B,) int32, recon (B,N,V) float32, mse (B,) float32.
+    With overlap ((B,) ints) the constraint of viterbi_encode_constrained_v
+    (encode.py:328-389) applies with overlap_bits; start is -1 where no walk
+    meets it (the reference raises).
     """
     seq = _f32(seq)
     cb = _f32(cb)
@@ -189,9 +197,27 @@ def viterbi(seq, cb, L, KV, nthreads: int = 0):
     start = np.empty((B,), dtype=np.int32)
     recon = np.empty_like(seq)
     mse = np.empty((B,), dtype=np.float32)
+    ov = None if overlap is None else np.ascontiguousarray(np.broadcast_to(
+        np.asarray(overlap, dtype=np.int64), (B,)).astype(np.int32))
     _check(lib().oracle_viterbi(L, KV, V, B, N, _ptr(seq), _ptr(cb), _ptr(walk), _ptr(bits),
-                                 _ptr(start), _ptr(recon), _ptr(mse), nthreads), "viterbi")
+                                 _ptr(start), _ptr(recon), _ptr(mse), int(overlap_bits), _ptr(ov),
+                                 nthreads), "viterbi")
     return walk, bits, start, recon, mse
+
+
+def viterbi_tailbiting(seq, cb, L, k, V, nthreads: int = 0):
+    """Tail-biting encoder, Algorithm 4 as viterbi_encode_tailbiting_v restates it
+    (src/viterbi/encode.py:392-422; V = 1: :175-216), batched: rotate each
+    sequence right by N//2 steps, encode it unconstrained, take the top L - kV
+    bits of the rotated walk's state at step N//2 as the overlap, and encode the
+    original under that constraint.  seq (B, N, V).  Returns walk, bitstream,
+    start, recon, mse (as viterbi) and overlap (B,) int32."""
+    seq = _f32(seq)
+    B, N, _ = seq.shape
+    kV = k * V
+    walk_r, _, _, _, _ = viterbi(np.roll(seq, N // 2, axis=1), cb, L, kV, nthreads)
+    overlap = (walk_r[:, N // 2] >> kV).astype(np.int32)
+    return viterbi(seq, cb, L, kV, nthreads, overlap=overlap, overlap_bits=L - kV) + (overlap,)
 
 
 def decode(bitstream, start, cb, L, KV):

@@ -385,11 +385,21 @@ int oracle_bcjr_backward(int L, int KV, int V, int64_t B, int N, const float* se
 /* Viterbi (float32, direct form; src/viterbi/encode.py:250-307)              */
 /* ------------------------------------------------------------------------- */
 
+/* One sequence.  With cons != 0, the constraint of viterbi_encode_constrained_v
+ * (src/viterbi/encode.py:328-389): cum_0 of a state whose top ob bits differ
+ * from ov becomes INF (:350-352, :364-365), the final argmin runs over states
+ * whose bottom ob bits equal ov (:367-371), and a best cost >= INF/2 (the
+ * reference raises, :372-375) is reported as start = -1. */
 static int viterbi_one(const trellis_t* tr, const float* cb, const float* seq, int32_t* walk,
                        int32_t* bitstream, int32_t* start, float* recon, float* mse,
-                       float* cum, float* ncum, uint8_t* bp /* N x NT */) {
+                       float* cum, float* ncum, uint8_t* bp /* N x NT */, int cons, int ob,
+                       uint32_t ov_raw) {
     const int64_t S = tr->S, NT = tr->NT, R = tr->R;
-    const int KV = tr->KV, V = tr->V, N = tr->N;
+    const int KV = tr->KV, V = tr->V, N = tr->N, L = tr->L;
+    const float INF = 1e18f;
+    const uint32_t omask = (1u << ob) - 1u;
+    const uint32_t top_mask = omask << (L - ob), target_top = (ov_raw & omask) << (L - ob);
+    const uint32_t target_bottom = ov_raw & omask;
     for (int64_t s = 0; s < S; ++s) cum[s] = 0.0f;
     for (int t = 0; t < N; ++t) {
         const float* w = seq + (size_t)t * V;
@@ -413,11 +423,18 @@ static int viterbi_one(const trellis_t* tr, const float* cb, const float* seq, i
                 ncum[s] = best + local;
             }
         }
+        if (cons && t == 0)
+            for (int64_t s = 0; s < S; ++s)
+                if (((uint32_t)s & top_mask) != target_top) ncum[s] = INF;
         memcpy(cum, ncum, (size_t)S * sizeof(float));
     }
+    if (cons)
+        for (int64_t s = 0; s < S; ++s)
+            if (((uint32_t)s & omask) != target_bottom) cum[s] = INF;
     int64_t fs = 0;
     for (int64_t s = 1; s < S; ++s)
         if (cum[s] < cum[fs]) fs = s;
+    const int infeasible = cons && cum[fs] >= INF / 2;
     int64_t s = fs;
     walk[N - 1] = (int32_t)s;
     for (int t = N - 1; t > 0; --t) {
@@ -425,7 +442,7 @@ static int viterbi_one(const trellis_t* tr, const float* cb, const float* seq, i
         s = (int64_t)bp[(size_t)t * NT + j] * NT + j;
         walk[t - 1] = (int32_t)s;
     }
-    *start = (int32_t)((int64_t)bp[s >> KV] * NT + (s >> KV));
+    *start = infeasible ? -1 : (int32_t)((int64_t)bp[s >> KV] * NT + (s >> KV));
     double se = 0.0;
     for (int t = 0; t < N; ++t) {
         bitstream[t] = walk[t] & (int32_t)(R - 1);
@@ -440,11 +457,13 @@ static int viterbi_one(const trellis_t* tr, const float* cb, const float* seq, i
     return ORACLE_OK;
 }
 
+/* overlap: (B,) or NULL (unconstrained); overlap_bits in [0, L]. */
 int oracle_viterbi(int L, int KV, int V, int64_t B, int N, const float* seq, const float* cb,
                    int32_t* walk, int32_t* bitstream, int32_t* start, float* recon, float* mse,
-                   int nthreads) {
+                   int overlap_bits, const int32_t* overlap, int nthreads) {
     trellis_t tr;
     if (trellis_init(&tr, L, KV, V, N) || B < 0 || KV > 8) return ORACLE_EINVAL;
+    if (overlap && (overlap_bits < 0 || overlap_bits > L || overlap_bits > 31)) return ORACLE_EINVAL;
     set_threads(nthreads);
     int err = ORACLE_OK;
 #pragma omp parallel
@@ -460,7 +479,8 @@ int oracle_viterbi(int L, int KV, int V, int64_t B, int N, const float* seq, con
             for (int64_t b = 0; b < B; ++b) {
                 size_t o = (size_t)b * N;
                 viterbi_one(&tr, cb, seq + o * V, walk + o, bitstream + o, start + b, recon + o * V,
-                            mse + b, cum, ncum, bp);
+                            mse + b, cum, ncum, bp, overlap != NULL, overlap_bits,
+                            overlap ? (uint32_t)overlap[b] : 0u);
             }
         }
         free(cum); free(ncum); free(bp);

@@ -9,7 +9,12 @@ from .forward_backward import (  # noqa: F401
 )
 from .codes import make_1mad_codebook, make_3inst_codebook, make_hyb_codebook_gpu  # noqa: F401
 from .viterbi import (  # noqa: F401
-    viterbi_decode_v_batched, viterbi_encode_chunked, viterbi_encode_v_batched_cuda, viterbi_encode_v_batched_hip,
+    viterbi_decode_v_batched, viterbi_encode_chunked, viterbi_encode_constrained_v_batched_hip,
+    viterbi_encode_tailbiting_v_batched_hip, viterbi_encode_v_batched_cuda, viterbi_encode_v_batched_hip,
+)
+from .encode import (  # noqa: F401
+    viterbi_decode, viterbi_decode_v, viterbi_encode, viterbi_encode_constrained, viterbi_encode_constrained_v,
+    viterbi_encode_tailbiting, viterbi_encode_tailbiting_v, viterbi_encode_v, viterbi_encode_v_batched,
 )
 from .quant import (  # noqa: F401
     bcjr_quantize_tiles, bcjr_quantize_weight, bcjr_quantize_weight_rotated, tile_for_viterbi, untile_from_viterbi,

@@ -165,9 +165,13 @@ def backward(spec: Spec, seq: torch.Tensor, T, table, g_soft, g_logZ=None):
         return d
 
 
-def viterbi(spec: Spec, seq: torch.Tensor, table, want_packed: bool = True):
+def viterbi(spec: Spec, seq: torch.Tensor, table, want_packed: bool = True, overlap=None,
+            overlap_bits: int | None = None):
     """Returns dict: walk, bitstream (B,N) int32; start (B,) int32; recon (B,N,V);
-    mse (B,); packed (B, ceil(N*kV/8)) uint8 (if kV divides 8 and want_packed)."""
+    mse (B,); packed (B, ceil(N*kV/8)) uint8 (if kV divides 8 and want_packed).
+    With overlap ((B,) int32 on the device) and overlap_bits, the tail-biting
+    constraint of bcjr_viterbi_constrained applies; start is -1 for a sequence
+    no walk satisfies."""
     with torch.cuda.device(seq.device):
         seq = seq.detach().to(torch.float32).contiguous()
         B, N, V = seq.shape
@@ -187,11 +191,21 @@ def viterbi(spec: Spec, seq: torch.Tensor, table, want_packed: bool = True):
             return out
         prob = spec.problem(B, N)
         ws = _workspace(prob, OP_VITERBI, dev)
-        _lib.check(_lib.load().bcjr_viterbi(
-            ctypes.byref(prob), _lib.ptr(seq), _lib.ptr(table), _lib.ptr(out["walk"]),
-            _lib.ptr(out["bitstream"]), _lib.ptr(out["start"]), _lib.ptr(out["recon"]),
-            _lib.ptr(out["mse"]), _lib.ptr(packed), _lib.ptr(ws), ws.numel(), _stream(dev)),
-            "bcjr_viterbi")
+        if overlap is None:
+            _lib.check(_lib.load().bcjr_viterbi(
+                ctypes.byref(prob), _lib.ptr(seq), _lib.ptr(table), _lib.ptr(out["walk"]),
+                _lib.ptr(out["bitstream"]), _lib.ptr(out["start"]), _lib.ptr(out["recon"]),
+                _lib.ptr(out["mse"]), _lib.ptr(packed), _lib.ptr(ws), ws.numel(), _stream(dev)),
+                "bcjr_viterbi")
+        else:
+            ov = torch.as_tensor(overlap, dtype=torch.int32, device=dev).reshape(-1).contiguous()
+            if ov.numel() != B:
+                raise AssertionError(f"overlap has {ov.numel()} values for B={B} sequences")
+            _lib.check(_lib.load().bcjr_viterbi_constrained(
+                ctypes.byref(prob), _lib.ptr(seq), _lib.ptr(table), int(overlap_bits), _lib.ptr(ov),
+                _lib.ptr(out["walk"]), _lib.ptr(out["bitstream"]), _lib.ptr(out["start"]),
+                _lib.ptr(out["recon"]), _lib.ptr(out["mse"]), _lib.ptr(packed), _lib.ptr(ws), ws.numel(),
+                _stream(dev)), "bcjr_viterbi_constrained")
         return out
 
 

@@ -41,6 +41,63 @@ def viterbi_encode_v_batched_hip(sequences, codebook, L=16, k=2, V=2, return_all
     return res
 
 
+def _check_batch(sequences, codebook, L, V):
+    if not sequences.is_cuda:
+        raise AssertionError("sequences must be a GPU tensor")
+    if sequences.dtype != torch.float32 or codebook.dtype != torch.float32:
+        raise AssertionError("sequences and codebook must be float32")
+    if tuple(codebook.shape) != (1 << L, V):
+        raise AssertionError(f"codebook must be ({1 << L}, {V}); got {tuple(codebook.shape)}")
+    if sequences.dim() != 2 or sequences.shape[1] % V:
+        raise AssertionError(f"sequences must be (B, T) with T divisible by V={V}; got {tuple(sequences.shape)}")
+
+
+def viterbi_encode_constrained_v_batched_hip(sequences, codebook, overlap_values, overlap_bits=None,
+                                             L=16, k=2, V=2, return_all=False):
+    """Batched viterbi_encode_constrained_v (src/viterbi/encode.py:328-389): the
+    walk of sequence b starts in a state whose top overlap_bits bits equal
+    overlap_values[b] and ends in one whose bottom overlap_bits bits do
+    (overlap_bits defaults to L - k*V, the tail-biting overlap; at most that).
+
+    Returns (bitstreams, start_states, recons, mses) as viterbi_encode_v_batched_hip;
+    start_states[b] is -1 where no walk meets the constraint (the reference
+    raises RuntimeError there)."""
+    _check_batch(sequences, codebook, L, V)
+    kV = k * V
+    ob = L - kV if overlap_bits is None else int(overlap_bits)
+    B, T = sequences.shape
+    spec, table = _spec_for(codebook, L, k, V)
+    table = None if table is None else table.detach().contiguous()
+    ov = torch.as_tensor(overlap_values, dtype=torch.int64, device=sequences.device).reshape(-1)
+    if ov.numel() == 1:
+        ov = ov.expand(B)
+    out = ops.viterbi(spec, sequences.reshape(B, T // V, V), table, overlap=ov.to(torch.int32),
+                      overlap_bits=ob)
+    res = (out["bitstream"], out["start"], out["recon"].reshape(B, T), out["mse"])
+    return res + (out,) if return_all else res
+
+
+def viterbi_encode_tailbiting_v_batched_hip(sequences, codebook, L=16, k=2, V=2, return_all=False):
+    """Batched viterbi_encode_tailbiting_v (Algorithm 4, src/viterbi/encode.py:392-422;
+    V = 1: :175-216) in two Viterbi launches: every sequence rotated right by
+    N//2 steps and encoded, the top L - k*V bits of each rotated walk's state at
+    step N//2 taken as its overlap, the originals encoded under that
+    constraint.  Returns (bitstreams, start_states, recons, mses, overlaps (B,)
+    int32)."""
+    _check_batch(sequences, codebook, L, V)
+    kV = k * V
+    B, T = sequences.shape
+    N = T // V
+    spec, table = _spec_for(codebook, L, k, V)
+    table = None if table is None else table.detach().contiguous()
+    steps = sequences.reshape(B, N, V)
+    rot = ops.viterbi(spec, torch.roll(steps, N // 2, dims=1).contiguous(), table, want_packed=False)
+    overlap = (rot["walk"][:, N // 2] >> kV).to(torch.int32)
+    out = ops.viterbi(spec, steps, table, overlap=overlap, overlap_bits=L - kV)
+    res = (out["bitstream"], out["start"], out["recon"].reshape(B, T), out["mse"], overlap)
+    return res + (out,) if return_all else res
+
+
 def viterbi_encode_v_batched_cuda(sequences, codebook):
     """The reference's entry point (src/viterbi/cuda_kernel.py:166-220), fixed at
     L=16, k=2, V=2: sequences (B, T) float32 GPU tensor with T even, codebook
@@ -74,4 +131,5 @@ def viterbi_decode_v_batched(bitstreams, start_states, codebook, L=16, k=2, V=2,
 
 
 __all__ = ["viterbi_encode_v_batched_hip", "viterbi_encode_v_batched_cuda", "viterbi_encode_chunked",
-           "viterbi_decode_v_batched"]
+           "viterbi_decode_v_batched", "viterbi_encode_constrained_v_batched_hip",
+           "viterbi_encode_tailbiting_v_batched_hip"]

@@ -512,6 +512,40 @@ int bcjr_viterbi(const bcjr_problem* prob, const float* seq, const float* codebo
   return launch(pl, prob->B, ws_bytes, &P, stream);
 }
 
+int bcjr_viterbi_constrained(const bcjr_problem* prob, const float* seq, const float* codebook_or_lut,
+                             int overlap_bits, const int32_t* overlap, int32_t* walk, int32_t* bitstream,
+                             int32_t* start_state, float* recon, float* mse, uint8_t* packed, void* ws,
+                             size_t ws_bytes, hipStream_t stream) {
+  Plan pl;
+  int rc = make_plan(prob, OP_VIT, &pl);
+  if (rc) return rc;
+  if (overlap_bits < 0 || overlap_bits > prob->L - pl.KV)
+    return fail(BCJR_EINVAL, "overlap_bits=%d must lie in [0, L - k*V] = [0, %d]", overlap_bits,
+                prob->L - pl.KV);
+  if (prob->B == 0) return BCJR_OK;
+  if (!seq || !ws || !overlap) return fail(BCJR_EINVAL, "seq, overlap and ws must be non-NULL");
+  if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
+    return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  if (packed && 8 % pl.KV != 0) return fail(BCJR_EINVAL, "packing needs k*V to divide 8");
+  bcjr::VitParams P = {};
+  P.seq = seq;
+  P.table = codebook_or_lut;
+  P.walk = walk;
+  P.bits = bitstream;
+  P.start = start_state;
+  P.recon = recon;
+  P.mse = mse;
+  P.packed = packed;
+  P.ws = static_cast<uint8_t*>(ws);
+  P.overlap = overlap;
+  P.overlap_bits = overlap_bits;
+  P.B = prob->B;
+  P.N = (int)prob->N;
+  P.L = prob->L;
+  P.Q = prob->Q;
+  return launch(pl, prob->B, ws_bytes, &P, stream);
+}
+
 int bcjr_decode(const bcjr_problem* prob, const int32_t* bitstream, const uint8_t* packed,
                 const int32_t* start_state, const float* codebook_or_lut, int32_t* walk, float* recon,
                 hipStream_t stream) {

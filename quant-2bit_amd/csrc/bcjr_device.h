@@ -352,8 +352,13 @@ struct VitParams {
   float* mse;         // (B,) or null
   uint8_t* packed;    // (B, ceil(N*kV/8)) or null
   uint8_t* ws;        // slots x (N * NT) bytes of backpointers
+  // Tail-biting constraint (src/viterbi/encode.py:105-172), when overlap is
+  // non-null: s_0 >> (L - ob) == overlap[b] and s_{N-1} mod 2^ob == overlap[b]
+  // (ob = overlap_bits, overlap[b] < 2^ob); start[b] = -1 when no walk meets it.
+  const int32_t* overlap;  // (B,) or null
   long long B;
   int N, L, Q;
+  int overlap_bits;
 };
 
 struct DecParams {

@@ -21,6 +21,10 @@
 
 namespace bcjr {
 
+// The cost of a state the tail-biting constraint excludes (float32(1e18), as
+// in src/viterbi/encode.py:124); a sum with it rounds back to it.
+constexpr float kVitInf = 1e18f;
+
 // Strict (value, index) order: smaller value first, then lower index.
 __device__ __forceinline__ bool vi_less(float a, int ia, float b, int ib) {
   return (a < b) || (a == b && ia < ib);
@@ -98,6 +102,15 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
     uint8_t* bp = P.ws + (size_t)blockIdx.x * (size_t)N * (size_t)NT;
     const float* seqb = P.seq + (size_t)b * N * V;
     for (int i = tid; i < N * V; i += nthr) wbuf[i] = seqb[i];
+    // cum_{-1}, the vector step 0 reads: 0, or for a constrained sequence
+    // kVitInf where the top ob bits of the step-0 state differ from ov.  Those
+    // bits lie in s_0 >> kV (ob <= L - kV), so kVitInf + E_0(s) = kVitInf is the
+    // masked cum_0 of src/viterbi/encode.py:139-141 without touching the step.
+    const bool cons = P.overlap != nullptr;
+    const int ob = P.overlap_bits;
+    const uint32_t ov = cons ? (uint32_t)P.overlap[b] & ((1u << ob) - 1u) : 0u;  // masked as encode.py:136
+    for (int j = tid; j < NT; j += nthr)
+      rbuf[NT + j] = (cons && ((uint32_t)j >> (L - KV - ob)) != ov) ? kVitInf : 0.0f;
     __syncthreads();
 
     for (int t = 0; t < N; ++t) {
@@ -115,7 +128,7 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
           const int sub = q >> lgNB;
           float ri[R];
 #pragma unroll
-          for (int p = 0; p < R; ++p) ri[p] = t ? prev[p * NB + u] : 0.0f;
+          for (int p = 0; p < R; ++p) ri[p] = prev[p * NB + u];
           float ro[RO];
           uint32_t bpw = 0;
 #pragma unroll
@@ -175,7 +188,7 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
     float fbest = INFINITY;
     int fstate = 0x7fffffff;
     {
-      const float* prev = rbuf + (N & 1) * NT;  // written at step N-2
+      const float* prev = rbuf + (N & 1) * NT;  // written at step N-2 (cum_{-1} when N = 1)
       float w[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) w[v] = wbuf[(N - 1) * V + v];
@@ -190,7 +203,9 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
             const float d2 = d * d;
             e = e + d2;
           }
-          const float cum = (N > 1 ? prev[s >> KV] : 0.0f) + e;
+          float cum = prev[s >> KV] + e;
+          // end constraint: s_{N-1} mod 2^ob == ov (encode.py:149-154)
+          if (cons && ((uint32_t)s & ((1u << ob) - 1u)) != ov) cum = kVitInf;
           if (vi_less(cum, s, fbest, fstate)) {
             fbest = cum;
             fstate = s;
@@ -223,6 +238,9 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
       // Only a NaN input leaves no candidate; fall back to state 0 so the
       // traceback below always indexes inside the trellis.
       walkbuf[N - 1] = (bs >= 0 && bs < (NT << KV)) ? bs : 0;
+      // A constrained sequence whose best end still costs kVitInf has no walk
+      // meeting the constraint (encode.py:155-159): flagged through start.
+      redi[0] = (cons && !(bv < 0.5f * kVitInf)) ? 1 : 0;
     }
     __syncthreads();
 
@@ -276,7 +294,7 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
         se += d * d;
       }
     }
-    if (P.start && tid == 0) P.start[b] = walkbuf[0] >> KV;
+    if (P.start && tid == 0) P.start[b] = redi[0] ? -1 : walkbuf[0] >> KV;
     if (P.packed) {
       constexpr int per = 8 / KV;
       const int nbytes = (N * KV + 7) / 8;

@@ -197,3 +197,23 @@ def test_cosine_temperature_schedule():
     assert sched(5, 1, 1.0, 0.01) == 0.01
     mid = sched(50, 101, 2.0, 0.0)  # cos(pi/2) = 0: the midpoint is the mean
     assert abs(mid - 1.0) < 1e-12
+
+
+def test_precompute_tables_match_reference_loops():
+    """precompute_predecessors(_v) and precompute_codebook_v against the loops of
+    src/viterbi/encode.py:22-37, 218-247 restated on a small trellis."""
+    from bcjr import encode as E
+    for L, k, V in [(6, 2, 1), (8, 1, 2), (8, 2, 2)]:
+        kV = k * V
+        ref = np.zeros((1 << L, 1 << kV), np.int32)
+        for s in range(1 << L):
+            for p in range(1 << kV):
+                ref[s, p] = (p << (L - kV)) | (s >> kV)
+        got = E.precompute_predecessors_v(L, k, V)
+        assert got.dtype == np.int32 and np.array_equal(got, ref)
+    assert np.array_equal(E.precompute_predecessors(6, 2), E.precompute_predecessors_v(6, 2, 1))
+    cb = E.precompute_codebook_v(4, 2, lambda s: np.stack([s * 0.5, -(s * 1.0)], 1))
+    assert cb.dtype == np.float32 and cb.shape == (16, 2) and cb[3, 1] == -3.0
+    with pytest.raises(AssertionError, match="expected"):
+        E.precompute_codebook_v(4, 2, lambda s: s * 1.0)
+

@@ -189,6 +189,58 @@ def test_monolithic_wrapper_and_dtype(bcjr_mod, oracle):
     assert max_rel(x.grad.cpu().numpy(), oracle.bcjr_backward(seq, cb, T, L, 4, g)) < GRAD_TOL
 
 
+@pytest.mark.parametrize("B,N,loss", [(2, 8, "randn"), (4, 16, "sum")])
+def test_reference_node_gates_l16_kv4(bcjr_mod, oracle, B, N, loss):
+    """The shapes of the reference's own node gates at the module defaults (L=16,
+    k=2, V=2): B=2, N=8 with a random upstream gradient
+    (test_bcjr_monolithic_parity.py:23-53) and B=4, N=16 with loss soft.sum()
+    (test_bcjr_fast_parity.py:23-57); codebook randn(2^16, 2), T = 1.0 as a 0-d
+    device tensor, preds/succs passed as the callers pass them."""
+    _say(f"reference node gate B={B} N={N} loss={loss}")
+    from bcjr import bcjr_forward_backward, build_pred_succ_tables
+    L, k, V, T = 16, 2, 2, 1.0
+    rng = np.random.default_rng(100 + B)
+    seq = rng.standard_normal((B, N, V)).astype(np.float32)
+    cb = rng.standard_normal((1 << L, V)).astype(np.float32)
+    g = (rng.standard_normal((B, N, V)) if loss == "randn" else np.ones((B, N, V))).astype(np.float32)
+    preds, succs = build_pred_succ_tables(device="cuda")
+    x = torch.tensor(seq, device="cuda", requires_grad=True)
+    soft, logZ = bcjr_forward_backward(x, torch.tensor(cb, device="cuda"), torch.tensor(T, device="cuda"),
+                                       preds=preds, succs=succs)
+    (soft * torch.tensor(g, device="cuda")).sum().backward()
+    s_ref, z_ref = oracle.bcjr_forward(seq, cb, T, L, k * V)
+    assert max_rel(soft.detach().cpu().numpy(), s_ref) < SOFT_TOL
+    assert np.abs(logZ.detach().cpu().numpy() - z_ref).max() <= LOGZ_TOL * np.abs(z_ref).max()
+    assert max_rel(x.grad.cpu().numpy(), oracle.bcjr_backward(seq, cb, T, L, k * V, g)) < GRAD_TOL
+
+
+def test_toy_two_layer_gradients_reach_every_latent(bcjr_mod):
+    """Integration gate in the manner of test_llama_bcjr_toy.py:37-157 (every
+    W_latent gets a non-zero gradient): a two-layer MLP whose weights are soft-
+    quantized by bcjr_quantize_weight (RHT, BCJR at L=16 kV=4 HYB, inverse RHT),
+    one loss, one backward."""
+    _say("toy two-layer gradients")
+    lut = np.random.default_rng(2).standard_normal((512, 2)).astype(np.float32)
+    cb = bcjr_mod.make_hyb_codebook_gpu(lut, 9, 16, "cuda")
+    torch.manual_seed(0)
+    shapes = [(64, 32), (16, 64)]
+    latents = [(torch.randn(s, device="cuda") * 0.05).requires_grad_(True) for s in shapes]
+    signs = [(torch.tensor(bcjr_mod.make_sign_vector(s[0], 2 * i), device="cuda"),
+              torch.tensor(bcjr_mod.make_sign_vector(s[1], 2 * i + 1), device="cuda")) for i, s in enumerate(shapes)]
+    T = torch.tensor(0.3, device="cuda")
+    x = torch.randn(8, 32, device="cuda")
+    h = x
+    for W, (sl, sr) in zip(latents, signs):
+        Wq = bcjr_mod.bcjr_quantize_weight(W, sl, sr, cb, T)
+        assert Wq.shape == W.shape and torch.isfinite(Wq).all()
+        h = torch.nn.functional.gelu(h @ Wq.t())
+    loss = (h - torch.randn_like(h)).pow(2).mean()
+    loss.backward()
+    for W in latents:
+        assert W.grad is not None and torch.isfinite(W.grad).all()
+        assert (W.grad != 0).any() and W.grad.abs().max() > 0
+
+
 def test_quantize_weight_rotated(bcjr_mod, oracle):
     """Tile -> node -> untile around the RMS scale (bcjr_quant.py:125-156)."""
     _say("quantize_weight_rotated")

@@ -220,6 +220,57 @@ def test_viterbi_table1_band_1mad(oracle):
     assert 0.062 <= float(mse.mean()) <= 0.075
 
 
+@pytest.mark.parametrize("L,KV,V,N,ob", [(4, 2, 1, 5, 2), (6, 2, 1, 5, 4), (4, 1, 1, 7, 3), (6, 2, 2, 4, 3),
+                                         (6, 2, 1, 4, 6), (6, 2, 1, 1, 4)])
+def test_constrained_viterbi_matches_brute_force(oracle, L, KV, V, N, ob):
+    """The minimum-cost path among those whose first state has top ob bits = v
+    and whose last state has bottom ob bits = v (encode.py:328-389), for every v;
+    no such path <=> start = -1 (where the reference raises)."""
+    rng = np.random.default_rng(L * 31 + N + ob)
+    cb = rng.standard_normal((1 << L, V)).astype(np.float32)
+    seq1 = rng.standard_normal((N, V)).astype(np.float32)
+    paths = oracle.enumerate_paths(L, KV, N)
+    cost = ((cb[paths] - seq1[None]) ** 2).sum(axis=(1, 2))
+    vals = np.arange(1 << ob)
+    walk, _, start, _, _ = oracle.viterbi(np.repeat(seq1[None], len(vals), 0), cb, L, KV,
+                                          overlap=vals, overlap_bits=ob)
+    m = (1 << ob) - 1
+    for i, v in enumerate(vals):
+        ok = ((paths[:, 0] >> (L - ob)) == v) & ((paths[:, -1] & m) == v)
+        if not ok.any():
+            assert start[i] == -1, v
+            continue
+        best = np.flatnonzero(ok)[np.argmin(cost[ok])]
+        assert start[i] == paths[best, 0] >> KV
+        assert np.array_equal(walk[i], paths[best]), v
+
+
+def test_constrained_viterbi_zero_bits_is_unconstrained(oracle):
+    rng = np.random.default_rng(14)
+    cb = rng.standard_normal((1 << 10, 1)).astype(np.float32)
+    seq = rng.standard_normal((3, 40, 1)).astype(np.float32)
+    a = oracle.viterbi(seq, cb, 10, 2)
+    b = oracle.viterbi(seq, cb, 10, 2, overlap=[0, 0, 0], overlap_bits=0)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+
+
+def test_tailbiting_gate(oracle):
+    """The reference's tail-biting gate (test_viterbi.py:135-197) at L=12, k=2,
+    1MAD: every walk wraps around (s_0 >> k == s_{N-1} mod 2^(L-k) == overlap)
+    and the mean MSE is within 0.005 of the unconstrained encoder's."""
+    rng = np.random.default_rng(42)
+    L, k = 12, 2
+    cb = oracle.codebook(oracle.CODE_1MAD, L)
+    seq = rng.standard_normal((32, 256, 1)).astype(np.float32)
+    _, _, _, _, mse0 = oracle.viterbi(seq, cb, L, k)
+    walk, bits, start, recon, mse, ov = oracle.viterbi_tailbiting(seq, cb, L, k, 1)
+    assert (start >= 0).all()
+    assert np.array_equal(walk[:, 0] >> k, ov)
+    assert np.array_equal(walk[:, -1] & ((1 << (L - k)) - 1), ov)
+    assert abs(float(mse.mean()) - float(mse0.mean())) < 0.005
+
+
 # ------------------------------- codebooks -------------------------------
 
 @pytest.mark.parametrize("name,code", [("1mad", 1), ("3inst", 2), ("hyb", 3)])
