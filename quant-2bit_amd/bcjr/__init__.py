@@ -4,8 +4,9 @@ Python surface mirroring the reference's src/bcjr package; all compute runs in
 the gfx950 HIP kernels of libbcjr_hip.so (C ABI in include/bcjr_hip.h).
 """
 from .forward_backward import (  # noqa: F401
-    BcjrFunction, K_BITS, L_BITS, V_DIM, bcjr_forward_backward, bcjr_forward_backward_monolithic,
-    build_pred_succ_tables,
+    BcjrFunction, K_BITS, L_BITS, V_DIM, bcjr_forward_backward, bcjr_forward_backward_fast,
+    bcjr_forward_backward_monolithic, bcjr_forward_backward_monolithic_graphed, build_pred_succ_tables,
+    reset_mono_graph_cache,
 )
 from .codes import make_1mad_codebook, make_3inst_codebook, make_hyb_codebook_gpu  # noqa: F401
 from .viterbi import (  # noqa: F401
@@ -17,7 +18,8 @@ from .encode import (  # noqa: F401
     viterbi_encode_tailbiting, viterbi_encode_tailbiting_v, viterbi_encode_v, viterbi_encode_v_batched,
 )
 from .quant import (  # noqa: F401
-    bcjr_quantize_tiles, bcjr_quantize_weight, bcjr_quantize_weight_rotated, tile_for_viterbi, untile_from_viterbi,
+    bcjr_quantize_tiles, bcjr_quantize_weight, bcjr_quantize_weight_rotated, graphed_bcjr_chunk_forward,
+    reset_graph_cache, tile_for_viterbi, untile_from_viterbi,
 )
 from .rht import (  # noqa: F401
     apply_inverse_rht_batched, apply_inverse_rht_gpu, apply_rht_batched, apply_rht_gpu, hadamard_transform,

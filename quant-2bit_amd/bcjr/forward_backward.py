@@ -134,7 +134,33 @@ def bcjr_forward_backward_monolithic(sequences, codebook, T_temp,
     return soft, None
 
 
+def bcjr_forward_backward_fast(sequences, codebook, T_temp,
+                               L=L_BITS, k=K_BITS, V=V_DIM,
+                               preds=None, succs=None,
+                               return_internals=False):
+    """Drop-in for the no-checkpoint variant (src/bcjr/forward_backward_fast.py:75-...,
+    selected by BCJR_FAST): the same node, so the same values and gradients."""
+    return bcjr_forward_backward(sequences, codebook, T_temp, L=L, k=k, V=V, preds=preds, succs=succs,
+                                 return_internals=return_internals)
+
+
+def bcjr_forward_backward_monolithic_graphed(sequences, codebook, T_temp,
+                                             preds=None, succs=None,
+                                             return_internals=False,
+                                             L=L_BITS, k=K_BITS, V=V_DIM):
+    """Drop-in for src/bcjr/bcjr_monolithic_graph.py:41-81: (soft, None).  The
+    reference captures its ~4N launches in a CUDA graph (BCJR_MONO_GRAPH=1); this
+    node is one launch per direction with no host synchronisation, so a caller
+    may capture it but gains nothing from it here."""
+    return bcjr_forward_backward_monolithic(sequences, codebook, T_temp, L=L, k=k, V=V)
+
+
+def reset_mono_graph_cache():
+    """src/bcjr/bcjr_monolithic_graph.py:84-87.  No graphs are cached here."""
+
+
 __all__ = [
     "L_BITS", "K_BITS", "V_DIM", "build_pred_succ_tables", "bcjr_forward_backward",
-    "bcjr_forward_backward_monolithic", "BcjrFunction",
+    "bcjr_forward_backward_monolithic", "BcjrFunction", "bcjr_forward_backward_fast",
+    "bcjr_forward_backward_monolithic_graphed", "reset_mono_graph_cache",
 ]

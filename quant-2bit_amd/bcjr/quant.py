@@ -36,6 +36,24 @@ def untile_from_viterbi(recons, shape_info, shape_mn, Tx=TX, Ty=TY):
     return recons.reshape(n_col, m, Ty).permute(1, 0, 2).contiguous().reshape(m, n)
 
 
+def _bcjr_chunk_forward(sequences_chunk, codebook, T_temp, preds=None, succs=None):
+    """One node call returning soft (B, N, V) (bcjr_quant.py:63-82).  The
+    reference dispatches on BCJR_MONOLITHIC / BCJR_FAST to one of its
+    implementations; every one of them is this node here."""
+    soft, _ = bcjr_forward_backward(sequences_chunk, codebook, T_temp, preds=preds, succs=succs)
+    return soft
+
+
+def graphed_bcjr_chunk_forward(sequences, codebook, T_temp, preds=None, succs=None):
+    """Drop-in for src/bcjr/bcjr_graph.py:56-81 (BCJR_GRAPH): soft (B, N, V) from
+    the node, which needs no graph capture to avoid per-step launches."""
+    return _bcjr_chunk_forward(sequences, codebook, T_temp, preds, succs)
+
+
+def reset_graph_cache():
+    """src/bcjr/bcjr_graph.py:84-88.  No graphs are cached here."""
+
+
 def bcjr_quantize_tiles(sequences, codebook, T_temp, preds=None, succs=None,
                         chunk_size=BCJR_CHUNK, use_checkpoint=True,
                         L=L_BITS, k=K_BITS, V=V_DIM):
@@ -87,4 +105,5 @@ def bcjr_quantize_weight(W_latent, sign_l, sign_r, codebook, T_temp, preds=None,
 
 
 __all__ = ["TX", "TY", "tile_for_viterbi", "untile_from_viterbi", "bcjr_quantize_tiles",
-           "bcjr_quantize_weight_rotated", "bcjr_quantize_weight"]
+           "bcjr_quantize_weight_rotated", "bcjr_quantize_weight", "graphed_bcjr_chunk_forward",
+           "reset_graph_cache"]

@@ -214,6 +214,41 @@ def test_reference_node_gates_l16_kv4(bcjr_mod, oracle, B, N, loss):
     assert max_rel(x.grad.cpu().numpy(), oracle.bcjr_backward(seq, cb, T, L, k * V, g)) < GRAD_TOL
 
 
+def test_reference_variant_entry_points_are_the_node(bcjr_mod):
+    """The reference's alternative implementations (forward_backward_fast.py:75,
+    bcjr_graph.py:56, bcjr_monolithic_graph.py:41, bcjr_quant.py:63) are gated
+    against its eager node at 1e-3 (test_bcjr_{fast,graph,mono_graph}_parity.py);
+    here each is the same node, so values and gradients are identical."""
+    _say("variant entry points")
+    from bcjr.quant import _bcjr_chunk_forward
+    L, k, V, B, N = 12, 2, 2, 4, 16
+    rng = np.random.default_rng(7)
+    cb = torch.tensor(rng.standard_normal((1 << L, V)).astype(np.float32), device="cuda")
+    seq = rng.standard_normal((B, N, V)).astype(np.float32)
+    T = torch.tensor(1.0, device="cuda")
+    outs, grads = [], []
+    fns = [lambda x: bcjr_mod.bcjr_forward_backward(x, cb, T, L=L, k=k, V=V)[0],
+           lambda x: bcjr_mod.bcjr_forward_backward_fast(x, cb, T, L=L, k=k, V=V)[0],
+           lambda x: bcjr_mod.bcjr_forward_backward_monolithic_graphed(x, cb, T, L=L, k=k, V=V)[0]]
+    for fn in fns:
+        x = torch.tensor(seq, device="cuda", requires_grad=True)
+        soft = fn(x)
+        soft.sum().backward()
+        outs.append(soft.detach())
+        grads.append(x.grad)
+    for o, g in zip(outs[1:], grads[1:]):
+        assert torch.equal(o, outs[0]) and torch.equal(g, grads[0])
+    # the chunk forwards use the module defaults L=16, k=2, V=2, as in the reference
+    lut = np.random.default_rng(2).standard_normal((512, 2)).astype(np.float32)
+    cb16 = bcjr_mod.make_hyb_codebook_gpu(lut, 9, 16, "cuda")
+    x = torch.tensor(rng.standard_normal((2, 32, 2)).astype(np.float32), device="cuda")
+    ref = bcjr_mod.bcjr_forward_backward(x, cb16, T)[0]
+    assert torch.equal(bcjr_mod.graphed_bcjr_chunk_forward(x, cb16, T, None, None), ref)
+    assert torch.equal(_bcjr_chunk_forward(x, cb16, T), ref)
+    bcjr_mod.reset_graph_cache()
+    bcjr_mod.reset_mono_graph_cache()
+
+
 def test_toy_two_layer_gradients_reach_every_latent(bcjr_mod):
     """Integration gate in the manner of test_llama_bcjr_toy.py:37-157 (every
     W_latent gets a non-zero gradient): a two-layer MLP whose weights are soft-
