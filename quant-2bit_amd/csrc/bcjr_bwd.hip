@@ -71,11 +71,11 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
   float* wbuf = wsum + 2 * kMaxWaves;                               // N*V
   float* gbuf = wbuf + N * V;                                       // N*V
   float* apart = gbuf + N * V;                                      // 2*nwaves*(V+1) per-wave partials
-  float* lut = apart + 2 * nwaves * (V + 1);
+  // HYB: signed LUT (code_hyb_signed), 8-byte aligned
+  float* lut = reinterpret_cast<float*>(smem) + ((apart + 2 * nwaves * (V + 1) - reinterpret_cast<float*>(smem) + 1) & ~1);
 
   if constexpr (CODE == CODE_HYB) {
-    const int nl = 2 << P.Q;
-    for (int i = tid; i < nl; i += nthr) lut[i] = P.table[i];
+    stage_hyb_signed(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
     __syncthreads();
   }
 

@@ -71,18 +71,37 @@ __device__ __forceinline__ void code_hyb(uint32_t s, const float* lut, int Q, fl
   c1 = (x & 0x8000u) ? -b : b;
 }
 
-// The same codeword from 2^rep interleaved copies of the LUT in LDS: entry e of
-// copy k is the float2 at e * 2^rep + k.  With 16 copies, copy k sits in LDS
-// bank pair k whatever the entry, so a half-wave of lanes each reading copy
-// (lane mod 16) is at most 2-way conflicted instead of the ~5-way of 32 random
-// 8-byte reads of one copy.
-__device__ __forceinline__ void code_hyb_rep(uint32_t s, const float2* lut2, int Q, int rep, uint32_t copy,
-                                             float& c0, float& c1) {
+// The same codeword from a signed LUT: 2^(Q+1) float2 entries, entry i holding
+// (lut[i mod 2^Q].x, +-lut[i mod 2^Q].y) with the minus sign where bit Q of i is
+// set.  Bits [15-Q, 16) of x are the index and the sign bit together, so one
+// bit-field extract replaces the index mask and the sign select.
+__device__ __forceinline__ void code_hyb_signed(uint32_t s, const float2* lut2s, int Q, float& c0, float& c1) {
   const uint32_t x = __umul24(s, s) + s;
-  const uint32_t idx = (x >> (15 - Q)) & ((1u << Q) - 1u);
-  const float2 v = lut2[(idx << rep) | copy];
+  const float2 v = lut2s[(x >> (15 - Q)) & ((2u << Q) - 1u)];
   c0 = v.x;
-  c1 = (x & 0x8000u) ? -v.y : v.y;
+  c1 = v.y;
+}
+
+// Fills a signed LUT (code_hyb_signed) from the (2^Q, 2) table, threads tid of nthr.
+__device__ __forceinline__ void stage_hyb_signed(float2* dst, const float* table, int Q, int tid, int nthr) {
+  const int n = 2 << Q, mask = (1 << Q) - 1;
+  for (int i = tid; i < n; i += nthr) {
+    const int e = i & mask;
+    const float y = table[2 * e + 1];
+    dst[i] = make_float2(table[2 * e], (i >> Q) ? -y : y);
+  }
+}
+
+// code_hyb_signed from 2^rep interleaved copies of the signed LUT in LDS: entry
+// i of copy k is the float2 at i * 2^rep + k, so the lanes reading one copy
+// spread over the LDS banks instead of all 64 lanes gathering from one 4 KiB
+// table (about 5-way bank conflicts for random 8-byte reads).
+__device__ __forceinline__ void code_hyb_signed_rep(uint32_t s, const float2* lut2s, int Q, int rep,
+                                                    uint32_t copy, float& c0, float& c1) {
+  const uint32_t x = __umul24(s, s) + s;
+  const float2 v = lut2s[(((x >> (15 - Q)) & ((2u << Q) - 1u)) << rep) | copy];
+  c0 = v.x;
+  c1 = v.y;
 }
 
 // c(s) for the soft kernels.  `table` is the global (S, V) codebook for
@@ -172,7 +191,7 @@ __device__ __forceinline__ void raw_codeword(uint32_t xu, uint32_t off, uint32_t
 #pragma unroll
     for (int v = 0; v < V; ++v) h[v] = table[(size_t)s * V + v];
   } else {
-    code_hyb(s, lut, Q, h[0], h[1]);
+    code_hyb_signed(s, reinterpret_cast<const float2*>(lut), Q, h[0], h[1]);
   }
 }
 

@@ -61,11 +61,11 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   // diagnostics variant, of sum_s P log2 P (one more), double-buffered by step.
   constexpr int SP = V + 1;
   float* spart = wbuf + N * V;                                    // 2*nwaves*SP per-wave partials
-  float* lut = spart + 2 * nwaves * SP;                           // HYB LUT
+  // HYB: signed LUT (code_hyb_signed), 8-byte aligned
+  float* lut = reinterpret_cast<float*>(smem) + ((spart + 2 * nwaves * SP - reinterpret_cast<float*>(smem) + 1) & ~1);
 
   if constexpr (CODE == CODE_HYB) {
-    const int nl = 2 << P.Q;
-    for (int i = tid; i < nl; i += nthr) lut[i] = P.table[i];
+    stage_hyb_signed(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
     __syncthreads();
   }
 

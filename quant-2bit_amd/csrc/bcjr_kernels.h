@@ -56,7 +56,7 @@ inline size_t fwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, i
   const size_t NT = (size_t)1 << (L - KV);
   size_t b = 8u * (size_t)((N + 1) & ~1);          // C_t (double), padded to 16 bytes
   b += 4u * (2 * NT + 3 * 16 + (size_t)N * V + 2 * (size_t)nwaves * (V + 1));
-  if (code == 3) b += 4u * ((size_t)2 << Q);
+  if (code == 3) b += 8u + 8u * ((size_t)2 << Q);  // signed LUT, 8-byte aligned
   return b;
 }
 
@@ -64,23 +64,23 @@ inline size_t bwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, i
   const size_t NT = (size_t)1 << (L - KV);
   size_t b = 8u * (size_t)((N + 1) & ~1);
   b += 4u * (2 * NT + 4 * 16 + 2 * (size_t)N * V + 2 * (size_t)nwaves * (V + 1));
-  if (code == 3) b += 4u * ((size_t)2 << Q);
+  if (code == 3) b += 8u + 8u * ((size_t)2 << Q);  // signed LUT, 8-byte aligned
   return b;
 }
 
-// log2 of the HYB LUT copies the kV = 4 Viterbi keeps: 16, or as many as fit
-// 64 KiB (2^Q entries of 8 bytes).
-__host__ __device__ constexpr int hyb_lut_rep(int Q) { return 13 - Q < 4 ? 13 - Q : 4; }
+// log2 of the signed HYB LUT copies the kV = 4 Viterbi keeps: 8, or as many as
+// fit 64 KiB (2^(Q+1) entries of 8 bytes each).
+__host__ __device__ constexpr int hyb_lut_rep(int Q) { return 12 - Q < 3 ? 12 - Q : 3; }
 
-// rep_lut: a HYB LUT is staged as 2^hyb_lut_rep(Q) interleaved copies (the
-// uncached 1024-thread instances), else as one.
+// rep_lut: a HYB LUT is staged as 2^hyb_lut_rep(Q) interleaved copies of the
+// signed LUT (the uncached 1024-thread instances), else as one plain copy.
 inline size_t vit_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q, bool rep_lut) {
   const size_t NT = (size_t)1 << (L - KV);
   (void)nwaves;
   size_t b = 8u * 16;                                           // per-wave MSE partials
   b += 4u * (2 * NT + (size_t)N * V + 2 * 16 + (size_t)N);      // state, seq, argmin, walk
   b = (b + 15) & ~(size_t)15;
-  if (code == 3) b += 8u * ((size_t)1 << Q << (rep_lut ? hyb_lut_rep(Q) : 0));
+  if (code == 3) b += rep_lut ? 8u * ((size_t)2 << Q << hyb_lut_rep(Q)) : 8u * ((size_t)1 << Q);
   return b;
 }
 

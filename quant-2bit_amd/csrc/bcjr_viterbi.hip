@@ -58,29 +58,40 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
   float* redv = wbuf + N * V;                                  // kMaxWaves
   int* redi = reinterpret_cast<int*>(redv + kMaxWaves);        // kMaxWaves
   int* walkbuf = redi + kMaxWaves;                             // N
-  // HYB LUT (16-byte aligned): the uncached 1024-thread instances (kV = 4),
-  // which gather an entry per state and step, keep 2^rep interleaved copies read
-  // at copy (lane mod 2^rep) (code_hyb_rep); the others one copy.
+  // HYB LUT (16-byte aligned).  The uncached 1024-thread instances (kV = 4),
+  // which look up a codeword per state and step, keep the signed LUT
+  // (code_hyb_signed: index and sign in one bit field) as 2^rep interleaved
+  // copies, lane l reading copy l mod 2^rep (code_hyb_signed_rep); the others,
+  // whose codewords are cached or rarely formed, one plain copy.
+  constexpr bool kSignedRep = (CODE == CODE_HYB) && !CACHE && MAXT == 1024;
   const size_t lut_off = ((size_t)(reinterpret_cast<unsigned char*>(walkbuf + N) - smem) + 15) & ~(size_t)15;
   float2* lut2 = reinterpret_cast<float2*>(smem + lut_off);
   const float* lut = reinterpret_cast<const float*>(lut2);
-  const int rep = (!CACHE && MAXT == 1024) ? hyb_lut_rep(P.Q) : 0;
+  const int rep = kSignedRep ? hyb_lut_rep(P.Q) : 0;
   const uint32_t copy = (uint32_t)lane & ((1u << rep) - 1u);
-  // c(s) for the state loops: HYB through the copies, other codes as codeword().
+  // c(s) for the state loops: HYB through the LDS LUT, other codes as codeword().
   auto cword = [&](uint32_t s, float (&c)[V]) {
-    if constexpr (CODE == CODE_HYB) {
-      code_hyb_rep(s, lut2, P.Q, rep, copy, c[0], c[1]);
+    if constexpr (kSignedRep) {
+      code_hyb_signed_rep(s, lut2, P.Q, rep, copy, c[0], c[1]);
+    } else if constexpr (CODE == CODE_HYB) {
+      code_hyb(s, lut, P.Q, c[0], c[1]);
     } else {
       codeword<CODE, V>(s, P.table, lut, P.Q, c);
     }
   };
 
-  if constexpr (CODE == CODE_HYB) {
-    const int nl = (1 << P.Q) << rep;
+  if constexpr (kSignedRep) {
+    const int nl = (2 << P.Q) << rep, mask = (1 << P.Q) - 1;
     for (int i = tid; i < nl; i += nthr) {
-      const int e = i >> rep;
-      lut2[i] = make_float2(P.table[2 * e], P.table[2 * e + 1]);
+      const int si = i >> rep, e = si & mask;
+      const float y = P.table[2 * e + 1];
+      lut2[i] = make_float2(P.table[2 * e], (si >> P.Q) ? -y : y);
     }
+    __syncthreads();
+  } else if constexpr (CODE == CODE_HYB) {
+    const int nl = 2 << P.Q;
+    float* lutw = reinterpret_cast<float*>(lut2);
+    for (int i = tid; i < nl; i += nthr) lutw[i] = P.table[i];
     __syncthreads();
   }
 
