@@ -29,6 +29,12 @@
 // butterfly with any underflowed group (sum < kUnderflow) is recomputed against
 // the group maxima, rare at T >= kExactBelowT; below it every group uses them.
 // A unit is one whole butterfly: R inputs, R outputs, R*R states.
+//
+// The per-wave soft partials of a beta step are double-buffered in LDS and
+// summed (in wave order) at the start of the next step, so LDS does not grow
+// with N.  The diagnostics instance (INTERNALS) also writes P, log alpha and
+// log beta per state when asked, and the marginal entropy -sum_s P log P of
+// each step, accumulated beside the soft partials.
 #include "bcjr_device.h"
 #include "bcjr_kernels.h"
 

@@ -11,9 +11,12 @@
 //   start = bp_0(walk_0 >> kV) * NT + (walk_0 >> kV) = walk_0 >> kV,
 //   bitstream_t = walk_t & (2^kV - 1), recon_t = c(walk_t).
 // Min-sum has no transcendentals; the butterfly layout and the per-step LDS
-// exchange are those of the soft kernels.  Backpointers (one byte per reduced
-// state and step) go to the caller's workspace and are staged back through LDS,
-// eight rows at a time, for the traceback.
+// exchange are those of the soft kernels.  Backpointers (kV bits per reduced
+// state and step where a thread's outputs fill a byte or half-word, else one
+// byte) go to the caller's workspace and are staged back through LDS, as many
+// rows as the 2*NT-float state buffers hold (32 at L=16, kV=2), for the
+// traceback.  bcjr_viterbi_constrained adds the tail-biting constraint of
+// encode.py:328-389 through the initial cost vector and the final argmin.
 #pragma clang fp contract(off)
 
 #include "bcjr_device.h"
@@ -257,7 +260,7 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
 
     // Traceback.  Row t of bp holds argmin_p cum_t(p*NT + j), i.e. the best
     // predecessor of the states of step t+1, so walk_{t} = bp_t(walk_{t+1} >> kV)
-    // * NT + (walk_{t+1} >> kV).  Rows are staged in LDS, up to 8 at a time, and
+    // * NT + (walk_{t+1} >> kV).  Rows are staged in LDS, cap at a time, and
     // walked on one thread.
     const int cap = (int)((2 * (size_t)NT * sizeof(float)) / (size_t)row_bytes);
     uint8_t* stage = reinterpret_cast<uint8_t*>(rbuf);
