@@ -44,6 +44,9 @@ constexpr int kOuterUnroll = R <= 4 ? R : 1;
 template <int KV, int V, int CODE, int UPT, int CU>
 __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
   constexpr int R = 1 << KV;
+  // Butterflies whose slot inputs are in flight ahead of the beta sweep's use
+  // (3 or 4 measured no faster at L=16: the HBM latency is already covered).
+  constexpr int kSlotAhead = 2;
   using CT = CodeTraits<CODE>;
   // Butterflies of 2 or 4 states run fully unrolled with their slot-side
   // inputs prefetched in registers; 16-state butterflies loop over outputs and
@@ -343,14 +346,16 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
       };
       // The next two butterflies in consumption order (t descending, i
       // ascending).
-      float pa[R], pua[R], pb[R], pub[R];
+      // A shift register of the next kSlotAhead butterflies' (m~, mu) inputs.
+      float pf[kSlotAhead][R], pfu[kSlotAhead][R];
       if constexpr (kPair) {
-        load_vec<R>(slot_src(N - 1, 0), pa);
-        load_vec<R>(slot_src(N - 1, 0) + R, pua);
-        if (UPT > 1 || N > 1) {
-          const float* src = UPT > 1 ? slot_src(N - 1, 1) : slot_src(N - 2, 0);
-          load_vec<R>(src, pb);
-          load_vec<R>(src + R, pub);
+#pragma unroll
+        for (int d = 0; d < kSlotAhead; ++d) {
+          const int tt = N - 1 - d / UPT;
+          if (tt >= 0) {
+            load_vec<R>(slot_src(tt, d % UPT), pf[d]);
+            load_vec<R>(slot_src(tt, d % UPT) + R, pfu[d]);
+          }
         }
       }
       double D = 0.0;  // D_t
@@ -467,20 +472,23 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
 #pragma unroll
           for (int r = 0; r < R; ++r) {
             if constexpr (kPair) {
-              pm[r] = pa[r];
-              pmu[r] = pua[r];
-              pa[r] = pb[r];
-              pua[r] = pub[r];
+              pm[r] = pf[0][r];
+              pmu[r] = pfu[0][r];
+#pragma unroll
+              for (int d = 0; d + 1 < kSlotAhead; ++d) {
+                pf[d][r] = pf[d + 1][r];
+                pfu[d][r] = pfu[d + 1][r];
+              }
             }
             ni[r] = nx[r];
             nui[r] = nxu[r];
           }
-          if constexpr (kPair) {  // fetch the butterfly two ahead
-            const int tt = i + 2 < UPT ? t : t - 1 - (i + 2 - UPT) / UPT;
-            const int ii = i + 2 < UPT ? i + 2 : (i + 2 - UPT) % UPT;
+          if constexpr (kPair) {  // fetch the butterfly kSlotAhead ahead
+            const int tt = t - (i + kSlotAhead) / UPT;
+            const int ii = (i + kSlotAhead) % UPT;
             if (tt >= 0) {
-              load_vec<R>(slot_src(tt, ii), pb);
-              load_vec<R>(slot_src(tt, ii) + R, pub);
+              load_vec<R>(slot_src(tt, ii), pf[kSlotAhead - 1]);
+              load_vec<R>(slot_src(tt, ii) + R, pfu[kSlotAhead - 1]);
             }
           }
           if (i + 1 < UPT) read_in(i + 1, nx, nxu);
