@@ -388,7 +388,15 @@ def secondary_config(torch, bcjr, ops, dev, exp_peak, T, B=4096):
             "state_updates_per_s": 4.0 * cells / (fwd_s + bwd_s),
             "roofline": {"bound": "valu_exp", "achieved": per_cell * cells / (fwd_s + bwd_s) / 1e12,
                          "peak": exp_peak / 1e12, "unit": "Texp/s",
-                         "frac": per_cell * cells / (fwd_s + bwd_s) / exp_peak, "per_cell": per_cell}}
+                         "frac": per_cell * cells / (fwd_s + bwd_s) / exp_peak, "per_cell": per_cell},
+            # A Llama-3.2-1B layer at this shape (the reference's own training config: 237,568 tiles of
+            # 128 steps): the soft fwd+bwd and one Viterbi pack, scaled from the 4096-tile batch.  The
+            # reference's layer-step wall clocks (whole QAT steps, dominated by its BCJR) are context
+            # from its scripts, not a like-for-like measurement.
+            "layer_step_s": (fwd_s + bwd_s + vit_s) * LAYER_SEQS / B,
+            "reference_layer_step_s_context": {"H100 SXM": 1644, "RTX 4080 Laptop": 4920,
+                                               "source": "scripts/vast_resume_llama.sh:13-14, "
+                                                         "scripts/rung_matched_l4.sh:8"}}
 
 
 def dequant_estimate(torch, bcjr, ops, dev):
