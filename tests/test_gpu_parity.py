@@ -99,6 +99,8 @@ CASES = [
     (10, 1, 1, 64, 4, "table", 0.2),     # kV = 1
     (10, 1, 2, 64, 4, "hyb", 0.4),       # k = 1, V = 2 (kV = 2, 2-D)
     (16, 2, 1, 256, 2, "3inst", 0.1),    # single-tile config: L=16, 8 butterflies per thread
+    (16, 2, 1, 256, 2, "3inst", 1.0),    # its other two temperatures
+    (16, 2, 1, 256, 2, "3inst", 0.3),
     (16, 2, 1, 96, 2, "1mad", 0.05),
     (16, 2, 1, 128, 2, "3inst", 0.01),   # the float32 floor the reference states (T >= 1e-2)
     (16, 2, 2, 64, 2, "hyb", 0.1),       # reference QAT trellis (L=16, kV=4)
