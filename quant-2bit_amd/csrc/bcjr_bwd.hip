@@ -54,6 +54,9 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
   constexpr bool kPair = R <= 4;
   static_assert(CU == 0 || kPair, "codeword cache is for butterflies of at most 4 states");
   static_assert(CU <= UPT, "at most UPT cached butterflies");
+  constexpr bool kCol = CODE == CODE_HYB_COL;  // HYB column walk: one butterfly per thread
+  static_assert(!kCol || (KV == 4 && UPT == 1), "the column walk is for L = 16, kV = 4");
+  constexpr bool kColUnroll = kCol;  // outputs unrolled: immediate LUT offsets
 
   extern __shared__ __align__(16) unsigned char smem[];
   const int L = P.L, N = P.N;
@@ -80,6 +83,17 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
   if constexpr (CODE == CODE_HYB) {
     stage_hyb_signed(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
     __syncthreads();
+  } else if constexpr (kCol) {
+    stage_hyb_col(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
+    __syncthreads();
+  }
+  const unsigned char* lutb = reinterpret_cast<const unsigned char*>(lut);
+  // Column-walk bases of this thread's butterfly u = tid, input c (state R*u + c),
+  // for the beta sweep; the alpha sweep forms its output's base as it goes.
+  uint32_t cbs[kCol ? R : 1];
+  if constexpr (kCol) {
+#pragma unroll
+    for (int c = 0; c < R; ++c) cbs[c] = hyb_col_base((uint32_t)(R * min(tid, NB - 1) + c), P.Q);
   }
 
   // Raw codewords h of this thread's first CU butterflies (hc[i][p][c] for
@@ -187,8 +201,9 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
 
         // Output r of butterfly u: m~ and mu of state R*u + r from the shifted
         // inputs m[p] (maximum 0) and the raw mu inputs; returns the group sum.
+        // cb: the column-walk base of state R*u + r (kCol only).
         auto alpha_out = [&](auto shift_tag, int i, int r, uint32_t xu, int u, const float (&m)[R],
-                             const float (&mui)[R], float oout, float& mo, float& muo) -> float {
+                             const float (&mui)[R], float oout, float& mo, float& muo, uint32_t cb) -> float {
           constexpr bool SHIFT = decltype(shift_tag)::value;
           float a[R], phi[R];
 #pragma unroll
@@ -197,6 +212,10 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
             if (i < CU) {
 #pragma unroll
               for (int v = 0; v < V; ++v) h[v] = hc[i < CU ? i : 0][p][r][v];
+            } else if constexpr (kCol) {
+              const float2 cw = hyb_col_read(lutb, cb + hyb_col_step(p, r));
+              h[0] = cw.x;
+              h[1] = cw.y;
             } else {
               raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)r, (uint32_t)(p * NT + R * u + r), P.table,
                                     lut, P.Q, h);
@@ -276,13 +295,14 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
               float mo[R], muo[R], smin = 0.0f;
 #pragma unroll
               for (int r = 0; r < R; ++r) {
-                const float s = alpha_out(Fast{}, i, r, xu, u, m, mui, oout, mo[r], muo[r]);
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, mui, oout, mo[r], muo[r], 0u);
                 smin = r ? fminf(smin, s) : s;
               }
               if constexpr (!EXACT) {
                 if (smin < kUnderflow) {
 #pragma unroll
-                  for (int r = 0; r < R; ++r) alpha_out(std::true_type{}, i, r, xu, u, m, mui, oout, mo[r], muo[r]);
+                  for (int r = 0; r < R; ++r)
+                    alpha_out(std::true_type{}, i, r, xu, u, m, mui, oout, mo[r], muo[r], 0u);
                 }
               }
 #pragma unroll
@@ -290,12 +310,38 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
                 lds_pair(yi ^ koff(r)) = make_float2(mo[r], muo[r]);
                 tmax = fmaxf(tmax, mo[r]);
               }
+            } else if constexpr (kColUnroll) {
+              // Outputs unrolled, so every state's LUT offset is an immediate; a
+              // butterfly with an underflowed group is redone output by output
+              // (its inputs are in registers, its outputs overwrite the pairs).
+              float smin = 0.0f;
+#pragma unroll
+              for (int r = 0; r < R; ++r) {
+                float mo, muo;
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, mui, oout, mo, muo, cbs[r]);
+                smin = r ? fminf(smin, s) : s;
+                lds_pair(yi ^ koff(r)) = make_float2(mo, muo);
+                tmax = fmaxf(tmax, mo);
+              }
+              if constexpr (!EXACT) {
+                if (smin < kUnderflow) {
+#pragma unroll 1
+                  for (int r = 0; r < R; ++r) {
+                    float mo, muo;
+                    alpha_out(std::true_type{}, i, r, xu, u, m, mui, oout, mo, muo,
+                              hyb_col_base((uint32_t)(R * u + r), P.Q));
+                    lds_pair(yi ^ koff(r)) = make_float2(mo, muo);
+                    tmax = fmaxf(tmax, mo);
+                  }
+                }
+              }
             } else {
 #pragma unroll kOuterUnroll<R>
               for (int r = 0; r < R; ++r) {
                 float mo, muo;
-                const float s = alpha_out(Fast{}, i, r, xu, u, m, mui, oout, mo, muo);
-                if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, i, r, xu, u, m, mui, oout, mo, muo);
+                const uint32_t cb = kCol ? hyb_col_base((uint32_t)(R * u + r), P.Q) : 0u;
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, mui, oout, mo, muo, cb);
+                if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, i, r, xu, u, m, mui, oout, mo, muo, cb);
                 lds_pair(yi ^ koff(r)) = make_float2(mo, muo);
                 tmax = fmaxf(tmax, mo);
               }
@@ -406,6 +452,10 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
             if (i < CU) {
 #pragma unroll
               for (int v = 0; v < V; ++v) hh[c][v] = hc[i < CU ? i : 0][p][c][v];
+            } else if constexpr (kCol) {
+              const float2 cw = hyb_col_read(lutb, cbs[c] + hyb_col_step(p, c));
+              hh[c][0] = cw.x;
+              hh[c][1] = cw.y;
             } else {
               raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)c, (uint32_t)(p * NT + R * u + c), P.table,
                                     lut, P.Q, hh[c]);
@@ -541,6 +591,46 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
                 lds_pair(yi ^ koff(p)) = make_float2(no[p], nuo[p]);
                 tmax = fmaxf(tmax, no[p]);
               }
+            } else if constexpr (kColUnroll) {
+              // Outputs unrolled (immediate LUT offsets); the butterfly's gradient
+              // sums are redone when a group underflowed.
+              const float* src = slot_src(t, i);
+              float smin = 0.0f, ua0 = 0.0f, ua1[V];
+#pragma unroll
+              for (int v = 0; v < V; ++v) ua1[v] = 0.0f;
+#pragma unroll
+              for (int p = 0; p < R; ++p) {
+                float no, nuo, a0, a1[V];
+                const float pms = src[p] + kts, pmup = src[R + p];
+                const float s = beta_out(Fast{}, i, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
+                smin = p ? fminf(smin, s) : s;
+                ua0 += a0;
+#pragma unroll
+                for (int v = 0; v < V; ++v) ua1[v] += a1[v];
+                lds_pair(yi ^ koff(p)) = make_float2(no, nuo);
+                tmax = fmaxf(tmax, no);
+              }
+              if constexpr (!EXACT) {
+                if (smin < kUnderflow) {
+                  ua0 = 0.0f;
+#pragma unroll
+                  for (int v = 0; v < V; ++v) ua1[v] = 0.0f;
+#pragma unroll 1
+                  for (int p = 0; p < R; ++p) {
+                    float no, nuo, a0, a1[V];
+                    const float pms = src[p] + kts, pmup = src[R + p];
+                    beta_out(std::true_type{}, i, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
+                    ua0 += a0;
+#pragma unroll
+                    for (int v = 0; v < V; ++v) ua1[v] += a1[v];
+                    lds_pair(yi ^ koff(p)) = make_float2(no, nuo);
+                    tmax = fmaxf(tmax, no);
+                  }
+                }
+              }
+              A0 += ua0;
+#pragma unroll
+              for (int v = 0; v < V; ++v) A1[v] += ua1[v];
             } else {
               const float* src = slot_src(t, i);
 #pragma unroll kOuterUnroll<R>
@@ -609,6 +699,7 @@ const void* bwd_kernel_ptr(int KV, int V, int code, int upt) {
   BCJR_BWD_CASE(4, 1, CODE_3INST, 1)
   BCJR_BWD_CASE(4, 2, CODE_TABLE, 1)
   BCJR_BWD_CASE(4, 2, CODE_HYB, 1)
+  BCJR_BWD_CASE(4, 2, CODE_HYB_COL, 1)
   return nullptr;
 }
 

@@ -254,13 +254,14 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
   pl->upt = upt;
   const int nwaves = nthr / 64;
   const int N = (int)p->N;
+  const int kcode = bcjr::soft_kernel_code(p->code, p->L, KV, p->Q);  // soft kernels only
   if (op == OP_FWD || op == OP_FWD_INTERNALS || op == OP_VIT) {
     const bool fwd = (op != OP_VIT);
     // The Viterbi kernel caches all of a thread's codewords in VGPRs up to 128
     // of them; the soft forward's cache is fixed per instance
     // (fwd_cached_units).
     pl->cache = !fwd && (pl->NSUB == 1) && (upt * R * R * p->V <= 128);
-    pl->fn = fwd ? bcjr::fwd_kernel_ptr(KV, p->V, p->code, upt, op == OP_FWD_INTERNALS)
+    pl->fn = fwd ? bcjr::fwd_kernel_ptr(KV, p->V, kcode, upt, op == OP_FWD_INTERNALS)
                  : bcjr::vit_kernel_ptr(KV, p->V, p->code, upt, pl->cache, false);
     if (!fwd && pl->NU >= 1024) {
       // 1024 threads (four waves per SIMD instead of two) when an instance
@@ -275,15 +276,15 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
         pl->upt = upt_w;
       }
     }
-    pl->lds = fwd ? bcjr::fwd_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q)
+    pl->lds = fwd ? bcjr::fwd_lds_bytes(p->L, KV, p->V, N, nwaves, kcode, p->Q)
                   : bcjr::vit_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q,
                                         !pl->cache && pl->nthr == 1024);
     pl->slot_bytes = fwd ? (size_t)N * pl->NT * sizeof(float) : (size_t)N * pl->NT;
   } else {
     pl->cache = false;
     pl->swz = pick_swizzle(p->L, KV);
-    pl->fn = bcjr::bwd_kernel_ptr(KV, p->V, p->code, upt);
-    pl->lds = bcjr::bwd_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q);
+    pl->fn = bcjr::bwd_kernel_ptr(KV, p->V, kcode, upt);
+    pl->lds = bcjr::bwd_lds_bytes(p->L, KV, p->V, N, nwaves, kcode, p->Q);
     pl->slot_bytes = (size_t)N * 2 * pl->NT * sizeof(float);
   }
   pl->slot_bytes = (pl->slot_bytes + 255) & ~(size_t)255;

@@ -26,7 +26,10 @@
 
 namespace bcjr {
 
-enum { CODE_TABLE = 0, CODE_1MAD = 1, CODE_3INST = 2, CODE_HYB = 3 };
+// CODE_HYB_COL is HYB with its LUT staged for the column walk (hyb_col_base);
+// the soft kernels take it at L = 16, kV = 4, 3 <= Q <= 9.  It never crosses the
+// C ABI.
+enum { CODE_TABLE = 0, CODE_1MAD = 1, CODE_3INST = 2, CODE_HYB = 3, CODE_HYB_COL = 4 };
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr double kLn2 = 0.6931471805599453;
@@ -89,6 +92,57 @@ __device__ __forceinline__ void stage_hyb_signed(float2* dst, const float* table
     const int e = i & mask;
     const float y = table[2 * e + 1];
     dst[i] = make_float2(table[2 * e], (i >> Q) ? -y : y);
+  }
+}
+
+// Column walk of the HYB LUT (L = 16, kV = 4, 3 <= Q <= 9).  State
+// s = p * 4096 + r (p < 16, r < 4096) has x = s^2 + s = x(r) + 2^12 * p * (2r + 1)
+// (mod 2^16): p moves only bits [12, 16) of x.  The LUT index, bits [15-Q, 16) of
+// x, splits into a column, bits [15-Q, 12), fixed by r, and a row, bits [12, 16)
+// (its top bit the sign bit), which steps by 2r + 1 (odd, so every row once) per
+// unit of p.  The signed LUT is staged as 32 rows of 64 float2 (512 bytes a row),
+// rows 16..31 repeating rows 0..15, so state s is the float2 at byte
+//   hyb_col_base(r) + hyb_col_step(p, r mod 8)
+// without a wrap: a per-lane base per butterfly output and a uniform step per p,
+// in place of the multiply, field extract and address arithmetic of each state.
+constexpr int kHybColBytes = 32 * 64 * 8;
+
+__device__ __forceinline__ uint32_t hyb_col_base(uint32_t r, int Q) {
+  const uint32_t x = __umul24(r, r) + r;
+  return (((x >> (15 - Q)) & ((1u << (Q - 3)) - 1u)) << 3) | (((x >> 12) & 15u) << 9);
+}
+
+// 2r + 1 mod 16 depends on r mod 8 only, so the step is uniform when r is a
+// butterfly's output index (state R*u + r, R = 16).
+__device__ __forceinline__ uint32_t hyb_col_step(int p, int r) {
+  return ((uint32_t)(p * (2 * r + 1)) & 15u) << 9;
+}
+
+__device__ __forceinline__ float2 hyb_col_read(const unsigned char* lutb, uint32_t off) {
+  return *reinterpret_cast<const float2*>(lutb + off);
+}
+
+// Any state from the column-walk LUT (rows 0..15).
+__device__ __forceinline__ void code_hyb_col(uint32_t s, const float2* lut2c, int Q, float& c0, float& c1) {
+  const uint32_t x = __umul24(s, s) + s;
+  const float2 v = lut2c[(((x >> 12) & 15u) << 6) | ((x >> (15 - Q)) & ((1u << (Q - 3)) - 1u))];
+  c0 = v.x;
+  c1 = v.y;
+}
+
+// Fills the column-walk LUT from the (2^Q, 2) table: entry (row, col) is signed
+// entry col + 2^(Q-3) * (row mod 16); columns past 2^(Q-3) are never read.
+__device__ __forceinline__ void stage_hyb_col(float2* dst, const float* table, int Q, int tid, int nthr) {
+  const int ncol = 1 << (Q - 3), mask = (1 << Q) - 1;
+  for (int k = tid; k < 32 * 64; k += nthr) {
+    const int col = k & 63, i = col + ncol * ((k >> 6) & 15);
+    float2 v = make_float2(0.0f, 0.0f);
+    if (col < ncol) {
+      const int e = i & mask;
+      const float y = table[2 * e + 1];
+      v = make_float2(table[2 * e], (i >> Q) ? -y : y);
+    }
+    dst[k] = v;
   }
 }
 
@@ -190,6 +244,8 @@ __device__ __forceinline__ void raw_codeword(uint32_t xu, uint32_t off, uint32_t
   } else if constexpr (CODE == CODE_TABLE) {
 #pragma unroll
     for (int v = 0; v < V; ++v) h[v] = table[(size_t)s * V + v];
+  } else if constexpr (CODE == CODE_HYB_COL) {
+    code_hyb_col(s, reinterpret_cast<const float2*>(lut), Q, h[0], h[1]);
   } else {
     code_hyb_signed(s, reinterpret_cast<const float2*>(lut), Q, h[0], h[1]);
   }

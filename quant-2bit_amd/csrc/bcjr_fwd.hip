@@ -48,6 +48,10 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   constexpr bool kPair = R <= 4;
   static_assert(CU == 0 || kPair, "codeword cache is for butterflies of at most 4 states");
   static_assert(CU <= UPT, "at most UPT cached butterflies");
+  constexpr bool kCol = CODE == CODE_HYB_COL;  // HYB column walk: one butterfly per thread
+  static_assert(!kCol || (KV == 4 && UPT == 1), "the column walk is for L = 16, kV = 4");
+  // Its outputs are unrolled except in the diagnostics instance, which would spill.
+  constexpr bool kColUnroll = kCol && !INTERNALS;
   using CT = CodeTraits<CODE>;
 
   extern __shared__ __align__(16) unsigned char smem[];
@@ -73,6 +77,17 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   if constexpr (CODE == CODE_HYB) {
     stage_hyb_signed(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
     __syncthreads();
+  } else if constexpr (kCol) {
+    stage_hyb_col(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
+    __syncthreads();
+  }
+  const unsigned char* lutb = reinterpret_cast<const unsigned char*>(lut);
+  // Column-walk bases of this thread's butterfly u = tid, input c (state R*u + c),
+  // for the beta sweep; the alpha sweep forms its output's base as it goes.
+  uint32_t cbs[kCol ? R : 1];
+  if constexpr (kCol) {
+#pragma unroll
+    for (int c = 0; c < R; ++c) cbs[c] = hyb_col_base((uint32_t)(R * min(tid, NB - 1) + c), P.Q);
   }
 
   // Raw codewords h of this thread's first CU butterflies, fixed for the
@@ -140,8 +155,9 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 
         // Output r of butterfly u (unit i) from the shifted inputs m[p]
         // (maximum 0): returns the group sum, mo = m~_t(R*u + r).
+        // cb: the column-walk base of state R*u + r (kCol only).
         auto alpha_out = [&](auto shift_tag, int i, int r, uint32_t xu, int u, const float (&m)[R], float oout,
-                             float& mo) -> float {
+                             float& mo, uint32_t cb) -> float {
           constexpr bool SHIFT = decltype(shift_tag)::value;
           float a[R];
 #pragma unroll
@@ -158,6 +174,10 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
               if (cached) {
 #pragma unroll
                 for (int v = 0; v < V; ++v) h[v] = hc[cached ? i : 0][p][r][v];
+              } else if constexpr (kCol) {
+                const float2 cw = hyb_col_read(lutb, cb + hyb_col_step(p, r));
+                h[0] = cw.x;
+                h[1] = cw.y;
               } else {
                 raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)r, (uint32_t)(p * NT + R * u + r), P.table,
                                       lut, P.Q, h);
@@ -215,24 +235,48 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
               float mo[R], smin = 0.0f;
 #pragma unroll
               for (int r = 0; r < R; ++r) {
-                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo[r]);
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo[r], 0u);
                 smin = r ? fminf(smin, s) : s;
               }
               if constexpr (!EXACT) {
                 if (smin < kUnderflow) {
 #pragma unroll
-                  for (int r = 0; r < R; ++r) alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo[r]);
+                  for (int r = 0; r < R; ++r) alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo[r], 0u);
                 }
               }
               store_vec<R>(cur + R * u, mo);
 #pragma unroll
               for (int r = 0; r < R; ++r) tmax = fmaxf(tmax, mo[r]);
+            } else if constexpr (kColUnroll) {
+              // Outputs unrolled, so every state's LUT offset is an immediate;
+              // a butterfly with an underflowed group is redone output by output.
+              float smin = 0.0f;
+#pragma unroll
+              for (int r = 0; r < R; ++r) {
+                float mo;
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, cbs[r]);
+                smin = r ? fminf(smin, s) : s;
+                cur[R * u + r] = mo;
+                tmax = fmaxf(tmax, mo);
+              }
+              if constexpr (!EXACT) {
+                if (smin < kUnderflow) {
+#pragma unroll 1
+                  for (int r = 0; r < R; ++r) {
+                    float mo;
+                    alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo, hyb_col_base((uint32_t)(R * u + r), P.Q));
+                    cur[R * u + r] = mo;
+                    tmax = fmaxf(tmax, mo);
+                  }
+                }
+              }
             } else {
 #pragma unroll 1
               for (int r = 0; r < R; ++r) {
                 float mo;
-                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo);
-                if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo);
+                const uint32_t cb = kCol ? hyb_col_base((uint32_t)(R * u + r), P.Q) : 0u;
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, cb);
+                if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo, cb);
                 cur[R * u + r] = mo;
                 tmax = fmaxf(tmax, mo);
               }
@@ -309,6 +353,10 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
             if (i < CU) {
 #pragma unroll
               for (int v = 0; v < V; ++v) hh[c][v] = hc[i < CU ? i : 0][p][c][v];
+            } else if constexpr (kCol) {
+              const float2 cw = hyb_col_read(lutb, cbs[c] + hyb_col_step(p, c));
+              hh[c][0] = cw.x;
+              hh[c][1] = cw.y;
             } else {
               raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)c, (uint32_t)(p * NT + R * u + c), P.table,
                                     lut, P.Q, hh[c]);
@@ -435,6 +483,46 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
                 cur[p * NB + u] = no[p];
                 tmax = fmaxf(tmax, no[p]);
               }
+            } else if constexpr (kColUnroll) {
+              // Outputs unrolled, so every state's LUT offset is an immediate;
+              // the butterfly's sums are redone when a group underflowed.
+              const float* src = slot_src(t, i);
+              float smin = 0.0f, ua[V], uh = 0.0f;
+#pragma unroll
+              for (int v = 0; v < V; ++v) ua[v] = 0.0f;
+#pragma unroll
+              for (int p = 0; p < R; ++p) {
+                float no, cs[V], hs;
+                const float pmr = src[p];
+                const float s = beta_out(Fast{}, i, p, xu, u, nr, n, pmr + kts, pmr, oout, no, cs, hs);
+                smin = p ? fminf(smin, s) : s;
+#pragma unroll
+                for (int v = 0; v < V; ++v) ua[v] += cs[v];
+                uh += hs;
+                cur[p * NB + u] = no;
+                tmax = fmaxf(tmax, no);
+              }
+              if constexpr (!EXACT) {
+                if (smin < kUnderflow) {
+                  uh = 0.0f;
+#pragma unroll
+                  for (int v = 0; v < V; ++v) ua[v] = 0.0f;
+#pragma unroll 1
+                  for (int p = 0; p < R; ++p) {
+                    float no, cs[V], hs;
+                    const float pmr = src[p];
+                    beta_out(std::true_type{}, i, p, xu, u, nr, n, pmr + kts, pmr, oout, no, cs, hs);
+#pragma unroll
+                    for (int v = 0; v < V; ++v) ua[v] += cs[v];
+                    uh += hs;
+                    cur[p * NB + u] = no;
+                    tmax = fmaxf(tmax, no);
+                  }
+                }
+              }
+              hacc += uh;
+#pragma unroll
+              for (int v = 0; v < V; ++v) acc[v] += ua[v];
             } else {
               const float* src = slot_src(t, i);
 #pragma unroll 1
@@ -516,6 +604,7 @@ const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool internals) {
   BCJR_FWD_CASE(4, 1, CODE_3INST, 1)
   BCJR_FWD_CASE(4, 2, CODE_TABLE, 1)
   BCJR_FWD_CASE(4, 2, CODE_HYB, 1)
+  BCJR_FWD_CASE(4, 2, CODE_HYB_COL, 1)
   return nullptr;
 }
 

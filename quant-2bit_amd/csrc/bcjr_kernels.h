@@ -51,12 +51,19 @@ hipError_t launch_fwht_tiled(const float* x, float* out, int batch, int m, int n
                              const float* post, const float* row_mid, const float* row_end, float scale,
                              int max_blocks, hipStream_t stream);
 
-// LDS bytes for one workgroup.
+// The kernel-side code of a soft launch: HYB at L = 16, kV = 4, 3 <= Q <= 9 takes
+// the column-walk LUT (code 4, CODE_HYB_COL in bcjr_device.h).
+inline int soft_kernel_code(int code, int L, int KV, int Q) {
+  return (code == 3 && L == 16 && KV == 4 && Q >= 3 && Q <= 9) ? 4 : code;
+}
+
+// LDS bytes for one workgroup (code as soft_kernel_code returns it).
 inline size_t fwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {
   const size_t NT = (size_t)1 << (L - KV);
   size_t b = 8u * (size_t)((N + 1) & ~1);          // C_t (double), padded to 16 bytes
   b += 4u * (2 * NT + 3 * 16 + (size_t)N * V + 2 * (size_t)nwaves * (V + 1));
   if (code == 3) b += 8u + 8u * ((size_t)2 << Q);  // signed LUT, 8-byte aligned
+  if (code == 4) b += 8u + 32u * 64u * 8u;         // column-walk LUT (32 rows of 64)
   return b;
 }
 
@@ -65,6 +72,7 @@ inline size_t bwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, i
   size_t b = 8u * (size_t)((N + 1) & ~1);
   b += 4u * (2 * NT + 4 * 16 + 2 * (size_t)N * V + 2 * (size_t)nwaves * (V + 1));
   if (code == 3) b += 8u + 8u * ((size_t)2 << Q);  // signed LUT, 8-byte aligned
+  if (code == 4) b += 8u + 32u * 64u * 8u;         // column-walk LUT (32 rows of 64)
   return b;
 }
 

@@ -217,3 +217,21 @@ def test_precompute_tables_match_reference_loops():
     with pytest.raises(AssertionError, match="expected"):
         E.precompute_codebook_v(4, 2, lambda s: s * 1.0)
 
+
+
+@pytest.mark.parametrize("Q", [3, 6, 9])
+def test_hyb_column_walk_identity(Q):
+    """The soft kernels' HYB column walk at L=16, kV=4: for every state
+    s = p*4096 + r, the float2 at byte col_base(r) + ((p*(2r+1)) mod 16) * 512 of
+    the 32 x 64 staged table is signed LUT entry bits [15-Q, 16) of s^2 + s
+    (src/qat/ste.py:376-392), without passing row 31."""
+    s = np.arange(1 << 16, dtype=np.uint64)
+    x = (s * s + s) & 0xFFFFFFFF
+    idx = (x >> (15 - Q)) & ((2 << Q) - 1)
+    p, r = s >> 12, s & 4095
+    x0 = (r * r + r) & 0xFFFFFFFF
+    base = (((x0 >> (15 - Q)) & ((1 << (Q - 3)) - 1)) << 3) | (((x0 >> 12) & 15) << 9)
+    byte = base + (((p * (2 * (r & 7) + 1)) & 15) << 9)
+    row, col = byte >> 9, (byte >> 3) & 63
+    assert row.max() < 32 and (byte & 7).max() == 0
+    assert np.array_equal(col + (1 << (Q - 3)) * (row & 15), idx)

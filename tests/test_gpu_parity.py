@@ -146,6 +146,30 @@ def test_backward_vs_oracle(bcjr_mod, oracle, L, k, V, N, B, kind, T):
     assert max_rel(x.grad.cpu().numpy(), d_ref) < GRAD_TOL
 
 
+@pytest.mark.parametrize("Q,T", [(9, 1.0), (9, 0.03), (3, 0.2), (6, 0.1), (10, 0.1)])
+def test_hyb_column_walk_vs_oracle(bcjr_mod, oracle, Q, T):
+    """HYB at L=16, kV=4 runs the soft kernels on the column-walk LUT for
+    3 <= Q <= 9 (Q = 10 keeps the signed LUT): forward and backward against the
+    oracle on the materialised codebook, in the fast and the low-temperature
+    (T < 0.08) variants."""
+    _say(f"HYB column walk Q={Q} T={T}")
+    from bcjr import bcjr_forward_backward
+    L, k, V, N, B = 16, 2, 2, 32, 2
+    rng = np.random.default_rng(100 + Q)
+    lut = rng.standard_normal((1 << Q, 2)).astype(np.float32)
+    cb = bcjr_mod.make_hyb_codebook_gpu(lut, Q=Q, L_bits=L, device="cuda")
+    cb_np = cb.cpu().numpy()
+    seq = rng.standard_normal((B, N, V)).astype(np.float32)
+    g = rng.standard_normal((B, N, V)).astype(np.float32)
+    x = torch.tensor(seq, device="cuda", requires_grad=True)
+    soft, logZ = bcjr_forward_backward(x, cb, T, L=L, k=k, V=V)
+    (soft * torch.tensor(g, device="cuda")).sum().backward()
+    s_ref, z_ref = oracle.bcjr_forward(seq, cb_np, T, L, k * V)
+    assert max_rel(soft.detach().cpu().numpy(), s_ref) < SOFT_TOL
+    assert np.abs(logZ.detach().cpu().numpy() - z_ref).max() <= LOGZ_TOL * np.abs(z_ref).max()
+    assert max_rel(x.grad.cpu().numpy(), oracle.bcjr_backward(seq, cb_np, T, L, k * V, g)) < GRAD_TOL
+
+
 def test_per_sequence_temperature(bcjr_mod, oracle):
     _say("per-sequence T")
     from bcjr import bcjr_forward_backward
