@@ -254,13 +254,14 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
   pl->upt = upt;
   const int nwaves = nthr / 64;
   const int N = (int)p->N;
-  const int kcode = bcjr::soft_kernel_code(p->code, p->L, KV, p->Q);  // soft kernels only
+  const int kcode = bcjr::soft_kernel_code(p->code, p->L, KV, p->Q);
   if (op == OP_FWD || op == OP_FWD_INTERNALS || op == OP_VIT) {
     const bool fwd = (op != OP_VIT);
     // The Viterbi kernel caches all of a thread's codewords in VGPRs up to 128
     // of them; the soft forward's cache is fixed per instance
     // (fwd_cached_units).
     pl->cache = !fwd && (pl->NSUB == 1) && (upt * R * R * p->V <= 128);
+    int vcode = p->code;  // the Viterbi instance's code
     pl->fn = fwd ? bcjr::fwd_kernel_ptr(KV, p->V, kcode, upt, op == OP_FWD_INTERNALS)
                  : bcjr::vit_kernel_ptr(KV, p->V, p->code, upt, pl->cache, false);
     if (!fwd && pl->NU >= 1024) {
@@ -268,8 +269,10 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
       // exists: codewords cached within 64 VGPRs, or none cached (kV = 4).
       const int upt_w = pl->NU / 1024;
       const bool cache_w = (pl->NSUB == 1) && (upt_w * R * R * p->V <= 64);
-      const void* fn_w = bcjr::vit_kernel_ptr(KV, p->V, p->code, upt_w, cache_w, true);
+      const int wcode = cache_w ? p->code : kcode;
+      const void* fn_w = bcjr::vit_kernel_ptr(KV, p->V, wcode, upt_w, cache_w, true);
       if (fn_w) {
+        vcode = wcode;
         pl->fn = fn_w;
         pl->cache = cache_w;
         pl->nthr = nthr = 1024;
@@ -277,7 +280,7 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
       }
     }
     pl->lds = fwd ? bcjr::fwd_lds_bytes(p->L, KV, p->V, N, nwaves, kcode, p->Q)
-                  : bcjr::vit_lds_bytes(p->L, KV, p->V, N, nwaves, p->code, p->Q,
+                  : bcjr::vit_lds_bytes(p->L, KV, p->V, N, nwaves, vcode, p->Q,
                                         !pl->cache && pl->nthr == 1024);
     pl->slot_bytes = fwd ? (size_t)N * pl->NT * sizeof(float) : (size_t)N * pl->NT;
   } else {

@@ -51,8 +51,9 @@ hipError_t launch_fwht_tiled(const float* x, float* out, int batch, int m, int n
                              const float* post, const float* row_mid, const float* row_end, float scale,
                              int max_blocks, hipStream_t stream);
 
-// The kernel-side code of a soft launch: HYB at L = 16, kV = 4, 3 <= Q <= 9 takes
-// the column-walk LUT (code 4, CODE_HYB_COL in bcjr_device.h).
+// The kernel-side code of a soft launch, or of a 1024-thread Viterbi launch:
+// HYB at L = 16, kV = 4, 3 <= Q <= 9 takes the column-walk LUT (code 4,
+// CODE_HYB_COL in bcjr_device.h).
 inline int soft_kernel_code(int code, int L, int KV, int Q) {
   return (code == 3 && L == 16 && KV == 4 && Q >= 3 && Q <= 9) ? 4 : code;
 }
@@ -89,6 +90,7 @@ inline size_t vit_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, i
   b += 4u * (2 * NT + (size_t)N * V + 2 * 16 + (size_t)N);      // state, seq, argmin, walk
   b = (b + 15) & ~(size_t)15;
   if (code == 3) b += rep_lut ? 8u * ((size_t)2 << Q << hyb_lut_rep(Q)) : 8u * ((size_t)1 << Q);
+  if (code == 4) b += 8u * (32u * 64u << 2);  // column-walk LUT, 4 interleaved copies
   return b;
 }
 

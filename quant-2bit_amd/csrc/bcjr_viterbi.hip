@@ -67,14 +67,26 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
   // copies, lane l reading copy l mod 2^rep (code_hyb_signed_rep); the others,
   // whose codewords are cached or rarely formed, one plain copy.
   constexpr bool kSignedRep = (CODE == CODE_HYB) && !CACHE && MAXT == 1024;
+  // CODE_HYB_COL (L = 16, kV = 4): the column-walk LUT (hyb_col_base) as
+  // 2^kColRep interleaved copies, so a state's codeword is the thread's base for
+  // its output plus a wave-uniform row step, with no per-state index arithmetic.
+  constexpr bool kColV = CODE == CODE_HYB_COL;
+  static_assert(!kColV || (KV == 4 && V == 2 && UPT == 1 && !CACHE), "the column walk is for L = 16, kV = 4");
+  constexpr int kColRep = 2;
   const size_t lut_off = ((size_t)(reinterpret_cast<unsigned char*>(walkbuf + N) - smem) + 15) & ~(size_t)15;
   float2* lut2 = reinterpret_cast<float2*>(smem + lut_off);
   const float* lut = reinterpret_cast<const float*>(lut2);
-  const int rep = kSignedRep ? hyb_lut_rep(P.Q) : 0;
+  const int rep = kSignedRep ? hyb_lut_rep(P.Q) : (kColV ? kColRep : 0);
   const uint32_t copy = (uint32_t)lane & ((1u << rep) - 1u);
   // c(s) for the state loops: HYB through the LDS LUT, other codes as codeword().
   auto cword = [&](uint32_t s, float (&c)[V]) {
-    if constexpr (kSignedRep) {
+    if constexpr (kColV) {
+      const uint32_t x = __umul24(s, s) + s;
+      const uint32_t e = (((x >> 12) & 15u) << 6) | ((x >> (15 - P.Q)) & ((1u << (P.Q - 3)) - 1u));
+      const float2 v = lut2[(e << kColRep) | copy];
+      c[0] = v.x;
+      c[1] = v.y;
+    } else if constexpr (kSignedRep) {
       code_hyb_signed_rep(s, lut2, P.Q, rep, copy, c[0], c[1]);
     } else if constexpr (CODE == CODE_HYB) {
       code_hyb(s, lut, P.Q, c[0], c[1]);
@@ -83,7 +95,20 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
     }
   };
 
-  if constexpr (kSignedRep) {
+  if constexpr (kColV) {
+    const int ncol = 1 << (P.Q - 3), mask = (1 << P.Q) - 1;
+    for (int i = tid; i < (32 * 64) << kColRep; i += nthr) {
+      const int k = i >> kColRep, col = k & 63, si = col + ncol * ((k >> 6) & 15);
+      float2 v = make_float2(0.0f, 0.0f);
+      if (col < ncol) {
+        const int e = si & mask;
+        const float y = P.table[2 * e + 1];
+        v = make_float2(P.table[2 * e], (si >> P.Q) ? -y : y);
+      }
+      lut2[i] = v;
+    }
+    __syncthreads();
+  } else if constexpr (kSignedRep) {
     const int nl = (2 << P.Q) << rep, mask = (1 << P.Q) - 1;
     for (int i = tid; i < nl; i += nthr) {
       const int si = i >> rep, e = si & mask;
@@ -109,6 +134,19 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
         for (int r = 0; r < R; ++r)
           cword((uint32_t)(p * NT + R * u + r), cw[i][p][r]);
     }
+  }
+
+  // Column-walk byte bases of this thread's RO outputs (unit tid: sub-butterfly
+  // tid >> lgNB, uniform over a wave, of butterfly tid mod NB).
+  const unsigned char* lutb = reinterpret_cast<const unsigned char*>(lut2);
+  uint32_t cbv[kColV ? RO : 1];
+  int sub4 = 0;
+  if constexpr (kColV) {
+    const int q0 = min(tid, NU - 1);
+    sub4 = __builtin_amdgcn_readfirstlane(q0 >> lgNB) * RO;
+#pragma unroll
+    for (int r = 0; r < RO; ++r)
+      cbv[r] = (hyb_col_base((uint32_t)(R * (q0 & (NB - 1)) + sub4 + r), P.Q) << kColRep) + (copy << 3);
   }
 
   const int row_bytes = PACK ? (NT * KV) >> 3 : NT;  // backpointer bytes per step
@@ -156,6 +194,10 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
               if constexpr (CACHE) {
 #pragma unroll
                 for (int v = 0; v < V; ++v) c[v] = cw[i][p][r][v];
+              } else if constexpr (kColV) {
+                const float2 cv = hyb_col_read(lutb, cbv[r] + (hyb_col_step(p, sub4 + r) << kColRep));
+                c[0] = cv.x;
+                c[1] = cv.y;
               } else {
                 cword((uint32_t)(p * NT + R * u + rr), c);
               }
@@ -681,6 +723,7 @@ const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache, bool wi
   BCJR_VIT_WIDE(4, 1, CODE_3INST, 1, false)
   BCJR_VIT_WIDE(4, 2, CODE_TABLE, 1, false)
   BCJR_VIT_WIDE(4, 2, CODE_HYB, 1, false)
+  BCJR_VIT_WIDE(4, 2, CODE_HYB_COL, 1, false)
   return nullptr;
 }
 

@@ -377,6 +377,26 @@ def test_viterbi_bit_exact(bcjr_mod, oracle, L, k, V, N, B, kind):
     assert (w3.cpu().numpy() == walk_r).all() and (r3.cpu().numpy() == recon_r.reshape(B, -1)).all()
 
 
+@pytest.mark.parametrize("Q", [3, 6, 9, 10])
+def test_viterbi_hyb_column_walk(bcjr_mod, oracle, Q):
+    """The 1024-thread Viterbi at L=16, kV=4 reads the column-walk LUT for
+    3 <= Q <= 9 (Q = 10: the signed LUT copies): bit-exact against the oracle."""
+    _say(f"viterbi HYB column walk Q={Q}")
+    from bcjr import viterbi_encode_v_batched_hip
+    L, k, V, N, B = 16, 2, 2, 48, 3
+    rng = np.random.default_rng(200 + Q)
+    lut = rng.standard_normal((1 << Q, 2)).astype(np.float32)
+    cb = bcjr_mod.make_hyb_codebook_gpu(lut, Q=Q, L_bits=L, device="cuda")
+    cb_np = cb.cpu().numpy()
+    seq = rng.standard_normal((B, N, V)).astype(np.float32)
+    bits, start, recon, mse, out = viterbi_encode_v_batched_hip(torch.tensor(seq.reshape(B, N * V), device="cuda"),
+                                                                cb, L=L, k=k, V=V, return_all=True)
+    walk_r, bits_r, start_r, recon_r, mse_r = oracle.viterbi(seq, cb_np, L, k * V)
+    assert np.array_equal(out["walk"].cpu().numpy(), walk_r)
+    assert np.array_equal(start.cpu().numpy(), start_r)
+    assert np.array_equal(recon.cpu().numpy(), recon_r.reshape(B, N * V))
+
+
 def test_viterbi_tie_rules(bcjr_mod, oracle):
     _say("viterbi ties")
     from bcjr import viterbi_encode_v_batched_hip
