@@ -170,6 +170,41 @@ def test_hyb_column_walk_vs_oracle(bcjr_mod, oracle, Q, T):
     assert max_rel(x.grad.cpu().numpy(), oracle.bcjr_backward(seq, cb_np, T, L, k * V, g)) < GRAD_TOL
 
 
+@pytest.mark.parametrize("L,k,V,kind", [(12, 2, 1, "1mad"), (16, 2, 1, "3inst"), (16, 2, 2, "hyb")])
+def test_short_and_empty_batches(bcjr_mod, oracle, L, k, V, kind):
+    """Edge shapes: sequences of 1, 2 and 3 steps (forward, backward and Viterbi
+    against the oracle) and an empty batch (empty outputs, zero-size gradient)."""
+    _say(f"short/empty L={L} k={k} V={V} {kind}")
+    from bcjr import bcjr_forward_backward, viterbi_encode_v_batched_hip
+    cb, cb_np = _codebook(bcjr_mod, oracle, kind, L, "cuda")
+    T = 0.2
+    for N in (1, 2, 3):
+        rng = np.random.default_rng(N)
+        seq = rng.standard_normal((2, N, V)).astype(np.float32)
+        g = rng.standard_normal((2, N, V)).astype(np.float32)
+        x = torch.tensor(seq, device="cuda", requires_grad=True)
+        soft, logZ = bcjr_forward_backward(x, cb, T, L=L, k=k, V=V)
+        (soft * torch.tensor(g, device="cuda")).sum().backward()
+        s_ref, z_ref = oracle.bcjr_forward(seq, cb_np, T, L, k * V)
+        assert max_rel(soft.detach().cpu().numpy(), s_ref) < SOFT_TOL
+        assert np.abs(logZ.detach().cpu().numpy() - z_ref).max() <= LOGZ_TOL * np.abs(z_ref).max()
+        assert max_rel(x.grad.cpu().numpy(), oracle.bcjr_backward(seq, cb_np, T, L, k * V, g)) < GRAD_TOL
+        bits, start, recon, mse, out = viterbi_encode_v_batched_hip(
+            torch.tensor(seq.reshape(2, N * V), device="cuda"), cb, L=L, k=k, V=V, return_all=True)
+        walk_r, _, start_r, recon_r, _ = oracle.viterbi(seq, cb_np, L, k * V)
+        assert np.array_equal(out["walk"].cpu().numpy(), walk_r)
+        assert np.array_equal(start.cpu().numpy(), start_r)
+        assert np.array_equal(recon.cpu().numpy(), recon_r.reshape(2, N * V))
+    x = torch.zeros((0, 8, V), device="cuda", requires_grad=True)
+    soft, logZ = bcjr_forward_backward(x, cb, T, L=L, k=k, V=V)
+    assert soft.shape == (0, 8, V) and logZ.shape == (0,)
+    soft.sum().backward()
+    assert x.grad.shape == (0, 8, V)
+    bits, start, recon, mse = viterbi_encode_v_batched_hip(torch.zeros((0, 8 * V), device="cuda"), cb,
+                                                           L=L, k=k, V=V)
+    assert bits.shape[0] == 0 and start.shape == (0,) and recon.shape == (0, 8 * V)
+
+
 def test_per_sequence_temperature(bcjr_mod, oracle):
     _say("per-sequence T")
     from bcjr import bcjr_forward_backward
