@@ -50,7 +50,8 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
   using CT = CodeTraits<CODE>;
   // Butterflies of 2 or 4 states run fully unrolled with their slot-side
   // inputs prefetched in registers; 16-state butterflies loop over outputs and
-  // read those inputs from the slot as they go.
+  // read those inputs from the slot as they go (the loop unrolled on the HYB
+  // column walk, whose LUT offsets are then immediates).
   constexpr bool kPair = R <= 4;
   static_assert(CU == 0 || kPair, "codeword cache is for butterflies of at most 4 states");
   static_assert(CU <= UPT, "at most UPT cached butterflies");
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
   float* wbuf = wsum + 2 * kMaxWaves;                               // N*V
   float* gbuf = wbuf + N * V;                                       // N*V
   float* apart = gbuf + N * V;                                      // 2*nwaves*(V+1) per-wave partials
-  // HYB: signed LUT (code_hyb_signed), 8-byte aligned
+  // HYB: signed LUT (code_hyb_signed) or column-walk LUT (hyb_col_base), 8-byte aligned
   float* lut = reinterpret_cast<float*>(smem) + ((apart + 2 * nwaves * (V + 1) - reinterpret_cast<float*>(smem) + 1) & ~1);
 
   if constexpr (CODE == CODE_HYB) {

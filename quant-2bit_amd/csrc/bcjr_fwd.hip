@@ -44,7 +44,8 @@ template <int KV, int V, int CODE, int UPT, int CU, bool INTERNALS>
 __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   constexpr int R = 1 << KV;
   // Butterflies of 2 or 4 states run fully unrolled with their slot inputs
-  // prefetched in registers; 16-state butterflies loop over outputs.
+  // prefetched in registers; 16-state butterflies loop over outputs (unrolled
+  // too on the HYB column walk, whose LUT offsets are then immediates).
   constexpr bool kPair = R <= 4;
   static_assert(CU == 0 || kPair, "codeword cache is for butterflies of at most 4 states");
   static_assert(CU <= UPT, "at most UPT cached butterflies");
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   // diagnostics variant, of sum_s P log2 P (one more), double-buffered by step.
   constexpr int SP = V + 1;
   float* spart = wbuf + N * V;                                    // 2*nwaves*SP per-wave partials
-  // HYB: signed LUT (code_hyb_signed), 8-byte aligned
+  // HYB: signed LUT (code_hyb_signed) or column-walk LUT (hyb_col_base), 8-byte aligned
   float* lut = reinterpret_cast<float*>(smem) + ((spart + 2 * nwaves * SP - reinterpret_cast<float*>(smem) + 1) & ~1);
 
   if constexpr (CODE == CODE_HYB) {
