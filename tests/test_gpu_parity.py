@@ -524,6 +524,35 @@ def test_bench_batch_spot_check_vs_oracle(bcjr_mod, oracle):
     assert (recon.cpu().numpy()[pick] == recon_r.reshape(len(pick), N)).all()
 
 
+def test_qat_shape_batch_spot_check_vs_oracle(bcjr_mod, oracle):
+    """The reference's QAT shape at the bench's size (L=16, k=2, V=2, HYB Q=9,
+    N=128, B=4096: the column-walk kernels, each workgroup reusing its slot for
+    ~5 sequences): four sequences against the oracle -- soft, log Z and gradient
+    at T=0.1, and the Viterbi path bit-exact."""
+    _say("QAT shape batch spot check B=4096")
+    from bcjr import bcjr_forward_backward, viterbi_encode_v_batched_hip
+    B, N, L, V = 4096, 128, 16, 2
+    rng = np.random.default_rng(3)
+    seq = rng.standard_normal((B, N, V)).astype(np.float32)
+    g = rng.standard_normal((B, N, V)).astype(np.float32)
+    cb, cb_np = _codebook(bcjr_mod, oracle, "hyb", L, "cuda")
+    x = torch.tensor(seq, device="cuda", requires_grad=True)
+    soft, logZ = bcjr_forward_backward(x, cb, 0.1, L=L, k=2, V=V)
+    (soft * torch.tensor(g, device="cuda")).sum().backward()
+    bits, start, recon, _, out = viterbi_encode_v_batched_hip(x.detach().reshape(B, N * V), cb, L=L, k=2, V=V,
+                                                              return_all=True)
+    pick = [0, 1, 2047, 4095]
+    s_ref, z_ref = oracle.bcjr_forward(seq[pick], cb_np, 0.1, L, 4)
+    d_ref = oracle.bcjr_backward(seq[pick], cb_np, 0.1, L, 4, g[pick])
+    assert max_rel(soft.detach().cpu().numpy()[pick], s_ref) < SOFT_TOL
+    assert np.abs(logZ.detach().cpu().numpy()[pick] - z_ref).max() <= LOGZ_TOL * np.abs(z_ref).max()
+    assert max_rel(x.grad.cpu().numpy()[pick], d_ref) < GRAD_TOL
+    walk_r, bits_r, start_r, recon_r, _ = oracle.viterbi(seq[pick], cb_np, L, 4)
+    assert (out["walk"].cpu().numpy()[pick] == walk_r).all()
+    assert (bits.cpu().numpy()[pick] == bits_r).all() and (start.cpu().numpy()[pick] == start_r).all()
+    assert (recon.cpu().numpy()[pick] == recon_r.reshape(len(pick), N * V)).all()
+
+
 def test_low_temperature_precision_bound(bcjr_mod, oracle):
     """Below T = 1e-2 float32 log-domain recursions lose precision as 1/T (the
     alpha/beta of a state on the final best path can lie ~1e4/T log2-units below
