@@ -42,7 +42,7 @@ template <int R>
 constexpr int kOuterUnroll = R <= 4 ? R : 1;
 
 template <int KV, int V, int CODE, int UPT, int CU>
-__global__ __launch_bounds__(512) void bcjr_bwd_kernel(BwdParams P) {
+__global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_COL ? 3 : 1) void bcjr_bwd_kernel(BwdParams P) {
   constexpr int R = 1 << KV;
   // Butterflies whose slot inputs are in flight ahead of the beta sweep's use
   // (3 or 4 measured no faster at L=16: the HBM latency is already covered).
