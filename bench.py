@@ -286,9 +286,11 @@ def read_traffic():
 
 
 def layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev):
-    """Seconds per Llama-3.2-1B decoder-layer QAT step: one forward + backward
-    over a B-sequence batch timed at each tensor's temperature, scaled by that
-    tensor's sequence count (the work per sequence does not depend on B)."""
+    """Seconds per Llama-3.2-1B decoder-layer QAT step, measured whole (every
+    tensor's sequences in one forward and one backward launch with per-sequence
+    T, one Viterbi launch, four RHTs per tensor), beside the per-tensor
+    breakdown: one forward + backward over a B-sequence batch timed at each
+    tensor's temperature, scaled by that tensor's sequence count."""
     spec, _ = bcjr.forward_backward._spec_for(cb, L, k, V)
     x = torch.randn(B, N, V, device=dev, generator=torch.Generator(dev).manual_seed(2))
     g = torch.randn(B, N, V, device=dev, generator=torch.Generator(dev).manual_seed(3))
@@ -334,15 +336,39 @@ def layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev):
         rht_s += 4 * one
         rht_rates[name] = {"ms": one * 1e3, "GB_s": 8.0 * rows * cols / one / 1e9}
         del Wt
+    # The same step measured whole: every tensor's sequences in one forward and
+    # one backward launch, each sequence carrying its tensor's T, then one
+    # Viterbi launch over all of them (237,568 sequences, ~1 GB of inputs and
+    # outputs).
+    del x, g
+    Ts = torch.cat([torch.full((rows * cols // 256,), T, device=dev) for _, rows, cols, T in LAYER_TENSORS])
+    X = torch.randn(LAYER_SEQS, N, V, device=dev, generator=torch.Generator(dev).manual_seed(4))
+    G = torch.randn(LAYER_SEQS, N, V, device=dev, generator=torch.Generator(dev).manual_seed(5))
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    ev[0].record(stream)
+    ops.forward(spec, X, Ts, None)
+    ops.backward(spec, X, Ts, None, G)
+    ev[1].record(stream)
+    ops.viterbi(spec, X, table)
+    ev[2].record(stream)
+    torch.cuda.synchronize(dev)
+    meas_soft = ev[0].elapsed_time(ev[1]) / 1e3
+    meas_vit = ev[1].elapsed_time(ev[2]) / 1e3
+    del X, G
     cells = float(LAYER_SEQS) * N * (1 << L)
-    return {"seconds": total + vit + rht_s, "soft_seconds": total, "viterbi_seconds": vit,
+    return {"seconds": meas_soft + meas_vit + rht_s,
+            "measured": {"soft_seconds": meas_soft, "viterbi_seconds": meas_vit,
+                         "state_updates_per_s": 4.0 * cells / meas_soft,
+                         "note": "one forward and one backward launch over all %d sequences with per-sequence T, "
+                                 "one Viterbi launch over all of them, plus the four RHTs per tensor" % LAYER_SEQS},
+            "estimate_seconds": total + vit + rht_s, "soft_seconds": total, "viterbi_seconds": vit,
             "rht_seconds": rht_s, "rht_per_tensor": rht_rates,
             "viterbi_ms_per_%d_sequences" % B: vit_batch_s * 1e3,
             "sequences": LAYER_SEQS, "tensors": per,
             "state_updates_per_s": 4.0 * cells / total,
-            "note": "fwd+bwd per tensor timed on a %d-sequence batch at that tensor's T, scaled by its "
-                    "sequence count, plus one Viterbi pack of every tile and four random Hadamard "
-                    "transforms per tensor" % B}
+            "note": "seconds: the measured whole-layer step; estimate_seconds: fwd+bwd per tensor timed on a "
+                    "%d-sequence batch at that tensor's T, scaled by its sequence count, plus one Viterbi pack of "
+                    "every tile and four random Hadamard transforms per tensor" % B}
 
 
 def secondary_config(torch, bcjr, ops, dev, exp_peak, T, B=4096):
@@ -380,6 +406,23 @@ def secondary_config(torch, bcjr, ops, dev, exp_peak, T, B=4096):
     e[1].record(stream)
     torch.cuda.synchronize(dev)
     vit_s = e[0].elapsed_time(e[1]) / 1e3 / reps
+    # A Llama-3.2-1B layer at this shape, measured whole: 237,568 tiles of 128
+    # steps in one forward and one backward launch, each tile at its tensor's T
+    # (q .05 ... down .5), then one Viterbi launch over all of them.
+    del x, g
+    Ts = torch.cat([torch.full((rows * cols // 256,), Tl, device=dev) for _, rows, cols, Tl in LAYER_TENSORS])
+    X = torch.randn(LAYER_SEQS, N, V, device=dev, generator=torch.Generator(dev).manual_seed(6))
+    G = torch.randn(LAYER_SEQS, N, V, device=dev, generator=torch.Generator(dev).manual_seed(7))
+    e[0].record(stream)
+    ops.forward(spec, X, Ts, table)
+    ops.backward(spec, X, Ts, table, G)
+    e[1].record(stream)
+    ops.viterbi(spec, X, table)
+    e[2].record(stream)
+    torch.cuda.synchronize(dev)
+    layer_soft_s = e[0].elapsed_time(e[1]) / 1e3
+    layer_vit_s = e[1].elapsed_time(e[2]) / 1e3
+    del X, G
     cells = float(B) * N * (1 << L)
     per_cell = trans_per_cell_grad(k * V)
     return {"workload": "reference QAT shape: L=16 k=2 V=2 (kV=4) N=128 B=%d, HYB, T=%g" % (B, T),
@@ -390,10 +433,12 @@ def secondary_config(torch, bcjr, ops, dev, exp_peak, T, B=4096):
                          "peak": exp_peak / 1e12, "unit": "Texp/s",
                          "frac": per_cell * cells / (fwd_s + bwd_s) / exp_peak, "per_cell": per_cell},
             # A Llama-3.2-1B layer at this shape (the reference's own training config: 237,568 tiles of
-            # 128 steps): the soft fwd+bwd and one Viterbi pack, scaled from the 4096-tile batch.  The
+            # 128 steps, per-tensor T), measured whole: the soft fwd+bwd and one Viterbi pack.  The
             # reference's layer-step wall clocks (whole QAT steps, dominated by its BCJR) are context
             # from its scripts, not a like-for-like measurement.
-            "layer_step_s": (fwd_s + bwd_s + vit_s) * LAYER_SEQS / B,
+            "layer_step_s": layer_soft_s + layer_vit_s,
+            "layer": {"soft_seconds": layer_soft_s, "viterbi_seconds": layer_vit_s,
+                      "estimate_at_T_%g_s" % T: (fwd_s + bwd_s + vit_s) * LAYER_SEQS / B},
             "reference_layer_step_s_context": {"H100 SXM": 1644, "RTX 4080 Laptop": 4920,
                                                "source": "scripts/vast_resume_llama.sh:13-14, "
                                                          "scripts/rung_matched_l4.sh:8"}}
