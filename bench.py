@@ -73,7 +73,7 @@ def parse():
     ap.add_argument("--T", type=float, default=0.1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=256, help="sequences in the CPU baseline sample")
-    ap.add_argument("--no-layer", action="store_true", help="skip the per-temperature layer estimate")
+    ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer steps (single-tile and reference QAT shapes)")
     ap.add_argument("--no-dequant", action="store_true", help="skip the dequant (on-disk format) leg")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the reference QAT shape (L=16, V=2, N=128, HYB) leg")
@@ -243,7 +243,7 @@ def main():
         layer = layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev)
     secondary = None
     if args.config == "tile" and not args.no_secondary:
-        secondary = secondary_config(torch, bcjr, ops, dev, exp_peak, args.T)
+        secondary = secondary_config(torch, bcjr, ops, dev, exp_peak, args.T, whole_layer=not args.no_layer)
     dequant = None
     if args.config == "tile" and not args.no_dequant:
         dequant = dequant_estimate(torch, bcjr, ops, dev)
@@ -371,7 +371,7 @@ def layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev):
                     "every tile and four random Hadamard transforms per tensor" % B}
 
 
-def secondary_config(torch, bcjr, ops, dev, exp_peak, T, B=4096):
+def secondary_config(torch, bcjr, ops, dev, exp_peak, T, B=4096, whole_layer=True):
     """The reference QAT shape as a secondary config: L=16, k=2, V=2 (kV=4), N=128
     steps, HYB codebook (random 2^9 x 2 LUT), B sequences of N(0,1) weights:
     forward + backward of the node, per-launch durations from HIP events, and
@@ -410,19 +410,9 @@ def secondary_config(torch, bcjr, ops, dev, exp_peak, T, B=4096):
     # steps in one forward and one backward launch, each tile at its tensor's T
     # (q .05 ... down .5), then one Viterbi launch over all of them.
     del x, g
-    Ts = torch.cat([torch.full((rows * cols // 256,), Tl, device=dev) for _, rows, cols, Tl in LAYER_TENSORS])
-    X = torch.randn(LAYER_SEQS, N, V, device=dev, generator=torch.Generator(dev).manual_seed(6))
-    G = torch.randn(LAYER_SEQS, N, V, device=dev, generator=torch.Generator(dev).manual_seed(7))
-    e[0].record(stream)
-    ops.forward(spec, X, Ts, table)
-    ops.backward(spec, X, Ts, table, G)
-    e[1].record(stream)
-    ops.viterbi(spec, X, table)
-    e[2].record(stream)
-    torch.cuda.synchronize(dev)
-    layer_soft_s = e[0].elapsed_time(e[1]) / 1e3
-    layer_vit_s = e[1].elapsed_time(e[2]) / 1e3
-    del X, G
+    layer_soft_s = layer_vit_s = None
+    if whole_layer:
+        layer_soft_s, layer_vit_s = _secondary_layer(torch, ops, spec, table, dev, N, V, stream, e)
     cells = float(B) * N * (1 << L)
     per_cell = trans_per_cell_grad(k * V)
     return {"workload": "reference QAT shape: L=16 k=2 V=2 (kV=4) N=128 B=%d, HYB, T=%g" % (B, T),
@@ -436,12 +426,28 @@ def secondary_config(torch, bcjr, ops, dev, exp_peak, T, B=4096):
             # 128 steps, per-tensor T), measured whole: the soft fwd+bwd and one Viterbi pack.  The
             # reference's layer-step wall clocks (whole QAT steps, dominated by its BCJR) are context
             # from its scripts, not a like-for-like measurement.
-            "layer_step_s": layer_soft_s + layer_vit_s,
+            "layer_step_s": layer_soft_s + layer_vit_s if whole_layer else None,
             "layer": {"soft_seconds": layer_soft_s, "viterbi_seconds": layer_vit_s,
                       "estimate_at_T_%g_s" % T: (fwd_s + bwd_s + vit_s) * LAYER_SEQS / B},
             "reference_layer_step_s_context": {"H100 SXM": 1644, "RTX 4080 Laptop": 4920,
                                                "source": "scripts/vast_resume_llama.sh:13-14, "
                                                          "scripts/rung_matched_l4.sh:8"}}
+
+
+def _secondary_layer(torch, ops, spec, table, dev, N, V, stream, e):
+    """Soft fwd+bwd seconds and Viterbi seconds of one whole Llama-3.2-1B layer at
+    the reference QAT shape (one launch each, per-sequence T)."""
+    Ts = torch.cat([torch.full((rows * cols // 256,), Tl, device=dev) for _, rows, cols, Tl in LAYER_TENSORS])
+    X = torch.randn(LAYER_SEQS, N, V, device=dev, generator=torch.Generator(dev).manual_seed(6))
+    G = torch.randn(LAYER_SEQS, N, V, device=dev, generator=torch.Generator(dev).manual_seed(7))
+    e[0].record(stream)
+    ops.forward(spec, X, Ts, table)
+    ops.backward(spec, X, Ts, table, G)
+    e[1].record(stream)
+    ops.viterbi(spec, X, table)
+    e[2].record(stream)
+    torch.cuda.synchronize(dev)
+    return e[0].elapsed_time(e[1]) / 1e3, e[1].elapsed_time(e[2]) / 1e3
 
 
 def dequant_estimate(torch, bcjr, ops, dev):
