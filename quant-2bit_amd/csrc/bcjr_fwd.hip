@@ -206,10 +206,20 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 
         // Inputs of butterfly tid + i*nthr; the next butterfly's are read
         // before the current one's arithmetic (prev is read-only this step).
+        // The column-walk instance keeps the reduced alpha state j at element
+        // j ^ ((j >> 5) & 15), so that its per-lane stores of 16 consecutive
+        // states (R*u + r) spread over the banks; for the reads j = p*NB + u
+        // (NB = 256) the XOR is (u >> 5) | 8 (p & 1), one base per parity.
         auto read_in = [&](int i, float (&m)[R]) {
           const int qq = min(tid + i * nthr, NB - 1);
+          if constexpr (kColUnroll) {
+            const int q0 = qq ^ (qq >> 5), q1 = q0 ^ 8;
 #pragma unroll
-          for (int p = 0; p < R; ++p) m[p] = prev[p * NB + qq];
+            for (int p = 0; p < R; ++p) m[p] = prev[p * NB + ((p & 1) ? q1 : q0)];
+          } else {
+#pragma unroll
+            for (int p = 0; p < R; ++p) m[p] = prev[p * NB + qq];
+          }
         };
         float nx[R];
         read_in(0, nx);
@@ -252,12 +262,13 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
               // Outputs unrolled, so every state's LUT offset is an immediate;
               // a butterfly with an underflowed group is redone output by output.
               float smin = 0.0f;
+              const int fu = (u >> 1) & (R - 1);  // the store XOR of state R*u + r
 #pragma unroll
               for (int r = 0; r < R; ++r) {
                 float mo;
                 const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, cbs[r]);
                 smin = r ? fminf(smin, s) : s;
-                cur[R * u + r] = mo;
+                cur[R * u + (r ^ fu)] = mo;
                 tmax = fmaxf(tmax, mo);
               }
               if constexpr (!EXACT) {
@@ -266,7 +277,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
                   for (int r = 0; r < R; ++r) {
                     float mo;
                     alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo, hyb_col_base((uint32_t)(R * u + r), P.Q));
-                    cur[R * u + r] = mo;
+                    cur[R * u + (r ^ fu)] = mo;
                     tmax = fmaxf(tmax, mo);
                   }
                 }
