@@ -105,7 +105,6 @@ __device__ __forceinline__ void stage_hyb_signed(float2* dst, const float* table
 //   hyb_col_base(r) + hyb_col_step(p, r mod 8)
 // without a wrap: a per-lane base per butterfly output and a uniform step per p,
 // in place of the multiply, field extract and address arithmetic of each state.
-constexpr int kHybColBytes = 32 * 64 * 8;
 
 __device__ __forceinline__ uint32_t hyb_col_base(uint32_t r, int Q) {
   const uint32_t x = __umul24(r, r) + r;
