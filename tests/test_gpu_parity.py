@@ -205,6 +205,36 @@ def test_short_and_empty_batches(bcjr_mod, oracle, L, k, V, kind):
     assert bits.shape[0] == 0 and start.shape == (0,) and recon.shape == (0, 8 * V)
 
 
+def test_longest_sequences_and_lds_limit(bcjr_mod, oracle):
+    """Maximum sizes at L=16, V=1 (3INST, T=0.1): the backward's longest
+    sequence (N = 2024) and the forward's (N = 2704) against the oracle, and one
+    step more is refused (BcjrError naming the LDS need) before any launch."""
+    _say("longest sequences L=16")
+    from bcjr import bcjr_forward_backward, make_3inst_codebook
+    from bcjr import ops
+    from bcjr._lib import BcjrError
+    L = 16
+    cb = make_3inst_codebook(L, "cuda")
+    cb_np = cb.cpu().numpy()
+    spec, _ = bcjr_mod.forward_backward._spec_for(cb, L, 2, 1)
+    rng = np.random.default_rng(11)
+    seq = rng.standard_normal((1, 2024, 1)).astype(np.float32)
+    g = rng.standard_normal((1, 2024, 1)).astype(np.float32)
+    x = torch.tensor(seq, device="cuda", requires_grad=True)
+    soft, logZ = bcjr_forward_backward(x, cb, 0.1, L=L, k=2, V=1)
+    (soft * torch.tensor(g, device="cuda")).sum().backward()
+    s_ref, z_ref = oracle.bcjr_forward(seq, cb_np, 0.1, L, 2)
+    assert max_rel(soft.detach().cpu().numpy(), s_ref) < SOFT_TOL
+    assert max_rel(x.grad.cpu().numpy(), oracle.bcjr_backward(seq, cb_np, 0.1, L, 2, g)) < GRAD_TOL
+    seq2 = rng.standard_normal((1, 2704, 1)).astype(np.float32)
+    soft2, _ = ops.forward(spec, torch.tensor(seq2, device="cuda"), 0.1, None)
+    assert max_rel(soft2.cpu().numpy(), oracle.bcjr_forward(seq2, cb_np, 0.1, L, 2)[0]) < SOFT_TOL
+    with pytest.raises(BcjrError, match="LDS"):
+        ops.forward(spec, torch.zeros((1, 2705, 1), device="cuda"), 0.1, None)
+    with pytest.raises(BcjrError, match="LDS"):
+        ops.backward(spec, torch.zeros((1, 2025, 1), device="cuda"), 0.1, None, torch.zeros((1, 2025, 1), device="cuda"))
+
+
 def test_per_sequence_temperature(bcjr_mod, oracle):
     _say("per-sequence T")
     from bcjr import bcjr_forward_backward
