@@ -170,6 +170,32 @@ def test_hyb_column_walk_vs_oracle(bcjr_mod, oracle, Q, T):
     assert max_rel(x.grad.cpu().numpy(), oracle.bcjr_backward(seq, cb_np, T, L, k * V, g)) < GRAD_TOL
 
 
+def test_hyb_column_walk_per_sequence_temperature(bcjr_mod, oracle):
+    """One launch of the column-walk kernels whose sequences take both variants
+    (T below and above 0.08) and the Viterbi over the same batch, against the
+    oracle sequence by sequence."""
+    _say("HYB column walk, per-sequence T")
+    from bcjr import bcjr_forward_backward, viterbi_encode_v_batched_hip
+    L, k, V, N = 16, 2, 2, 24
+    Ts = np.array([0.05, 0.3, 0.02, 1.0], np.float32)
+    B = len(Ts)
+    rng = np.random.default_rng(31)
+    cb, cb_np = _codebook(bcjr_mod, oracle, "hyb", L, "cuda")
+    seq = rng.standard_normal((B, N, V)).astype(np.float32)
+    g = rng.standard_normal((B, N, V)).astype(np.float32)
+    x = torch.tensor(seq, device="cuda", requires_grad=True)
+    soft, logZ = bcjr_forward_backward(x, cb, torch.tensor(Ts, device="cuda"), L=L, k=k, V=V)
+    (soft * torch.tensor(g, device="cuda")).sum().backward()
+    for b in range(B):
+        s_ref, z_ref = oracle.bcjr_forward(seq[b:b + 1], cb_np, float(Ts[b]), L, k * V)
+        d_ref = oracle.bcjr_backward(seq[b:b + 1], cb_np, float(Ts[b]), L, k * V, g[b:b + 1])
+        assert max_rel(soft[b:b + 1].detach().cpu().numpy(), s_ref) < SOFT_TOL
+        assert max_rel(x.grad[b:b + 1].cpu().numpy(), d_ref) < GRAD_TOL
+    bits, start, recon, mse, out = viterbi_encode_v_batched_hip(torch.tensor(seq.reshape(B, N * V), device="cuda"),
+                                                                cb, L=L, k=k, V=V, return_all=True)
+    assert np.array_equal(out["walk"].cpu().numpy(), oracle.viterbi(seq, cb_np, L, k * V)[0])
+
+
 @pytest.mark.parametrize("L,k,V,kind", [(12, 2, 1, "1mad"), (16, 2, 1, "3inst"), (16, 2, 2, "hyb")])
 def test_short_and_empty_batches(bcjr_mod, oracle, L, k, V, kind):
     """Edge shapes: sequences of 1, 2 and 3 steps (forward, backward and Viterbi
