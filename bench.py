@@ -167,7 +167,7 @@ def main():
     cb = bcjr.make_3inst_codebook(L, dev) if kind == "3inst" else bcjr.make_1mad_codebook(L, dev)
     x = torch.tensor(seq_np, device=dev)
     g = torch.tensor(g_np, device=dev)
-    spec, _ = bcjr.forward_backward._spec_for(cb, L, k, V)
+    spec, _ = bcjr.codes.resolve_codebook(cb, L, k, V, dev)
 
     def step():
         xs = x.detach().requires_grad_(True)
@@ -291,7 +291,7 @@ def layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev):
     T, one Viterbi launch, four RHTs per tensor), beside the per-tensor
     breakdown: one forward + backward over a B-sequence batch timed at each
     tensor's temperature, scaled by that tensor's sequence count."""
-    spec, _ = bcjr.forward_backward._spec_for(cb, L, k, V)
+    spec, _ = bcjr.codes.resolve_codebook(cb, L, k, V, dev)
     x = torch.randn(B, N, V, device=dev, generator=torch.Generator(dev).manual_seed(2))
     g = torch.randn(B, N, V, device=dev, generator=torch.Generator(dev).manual_seed(3))
     stream = torch.cuda.current_stream(dev)
@@ -309,7 +309,7 @@ def layer_estimate(torch, bcjr, ops, cb, L, k, V, N, B, dev):
         per[name] = {"T": T, "sequences": rows * cols // 256, "seconds": sec}
         total += sec
     # The T -> 0 Viterbi pack of every tile (walks, 2-bit bitstream) after the soft pass.
-    _, table = bcjr.forward_backward._spec_for(cb, L, k, V)
+    _, table = bcjr.codes.resolve_codebook(cb, L, k, V, dev)
     ops.viterbi(spec, x, table)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
@@ -380,7 +380,7 @@ def secondary_config(torch, bcjr, ops, dev, exp_peak, T, B=4096, whole_layer=Tru
     L, k, V, N = 16, 2, 2, 128
     lut = np.random.default_rng(3).standard_normal((512, 2)).astype(np.float32)
     cb = bcjr.make_hyb_codebook_gpu(lut, 9, L, dev)
-    spec, table = bcjr.forward_backward._spec_for(cb, L, k, V)
+    spec, table = bcjr.codes.resolve_codebook(cb, L, k, V, dev)
     x = torch.randn(B, N, V, device=dev, generator=torch.Generator(dev).manual_seed(4))
     g = torch.randn(B, N, V, device=dev, generator=torch.Generator(dev).manual_seed(5))
     stream = torch.cuda.current_stream(dev)

@@ -16,7 +16,8 @@ import math
 import torch
 
 from . import ops
-from .forward_backward import K_BITS, L_BITS, V_DIM, _as_table, _check_args, _spec_for
+from .codes import resolve_codebook
+from .forward_backward import K_BITS, L_BITS, V_DIM, _check_args
 from .quant import TX, TY, tile_for_viterbi
 from .rht import apply_rht_gpu
 from .ste import _f32_cuda, _quantized_linears, _rms, measure_ptq_residual
@@ -38,8 +39,8 @@ def bcjr_marginal_entropy(sequences, codebook, T_temp, L=L_BITS, k=K_BITS, V=V_D
     gradient.  Bounds: 0 <= H <= L ln 2, the upper one reached by the uniform
     marginals of T -> inf."""
     _check_args(sequences, codebook, L, k, V, None, None)
-    spec, table = _spec_for(codebook, L, k, V)
-    _, _, H = ops.forward_entropy(spec, sequences, T_temp, _as_table(spec, table))
+    spec, table = resolve_codebook(codebook, L, k, V, sequences.device)
+    _, _, H = ops.forward_entropy(spec, sequences, T_temp, table)
     return H
 
 

@@ -7,21 +7,36 @@ return values and assertion behaviour.  The whole forward (alpha and beta
 recursions, marginals, soft codeword, log Z) is one kernel launch, and the
 backward is one more; autograd saves only the inputs.
 
+The node is a pair of registered torch operators, bcjr::forward and
+bcjr::backward (torch.library.custom_op), with fake (meta) implementations and
+an autograd formula, so torch.compile traces through it without a graph break
+(the reference compiles its node: src/bcjr/forward_backward_fast.py:33-44,
+src/tripwires/test_bcjr_compile.py:28-84).
+
 Trellis (forward_backward.py:1-45): S = 2^L states, kV = k*V bits per step,
 next = ((s << kV) | c) & (S-1); emission ll_t(s) = -||c(s) - w_t||^2 / T;
 log_alpha_{-1} = 0 (free start), log_beta_{N-1} = 0 (free end).
 
-Codebooks.  `codebook` is the (2^L, V) float32 table, as in the reference.  A
-table made by bcjr.codes (make_1mad_codebook, make_3inst_codebook,
-make_hyb_codebook_gpu) carries its generator, and the kernels then hash c(s)
-in-kernel instead of reading the table; the values are bit-identical.
+Codebooks.  `codebook` is the (2^L, V) float32 table, as in the reference.  The
+kernels hash c(s) in-kernel for the 1MAD / 3INST codebooks and read a staged LUT
+for HYB ones, whether the table was made by bcjr.codes or recognised by content
+(bcjr.codes.resolve_codebook); any other table is read as a table.
+
+Temperature.  A python float, a 0-d / (1,) tensor, or a (B,) tensor (one value
+per sequence).  A python float becomes a one-element device tensor through a
+fill kernel, so the node makes no host-to-device copy and can be captured.  T
+must be finite and > 0: a sequence whose T is not, or whose weights (or, in the
+backward, upstream gradients) are not all finite, gets NaN outputs.
 """
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
+from torch import Tensor
 
 from . import ops
-from .ops import CODE_HYB, CODE_TABLE, Spec
+from .codes import resolve_codebook
 
 L_BITS = 16
 K_BITS = 2
@@ -43,18 +58,8 @@ def build_pred_succ_tables(L=L_BITS, k=K_BITS, V=V_DIM, device="cuda"):
     return preds, succs
 
 
-def _spec_for(codebook, L, k, V):
-    """Spec and the pointer source for the kernels (table, HYB LUT or None)."""
-    code = getattr(codebook, "_bcjr_code", CODE_TABLE)
-    if code == CODE_TABLE:
-        return Spec(L, k, V, CODE_TABLE), codebook
-    if code == CODE_HYB:
-        return Spec(L, k, V, CODE_HYB, int(codebook._bcjr_Q)), codebook._bcjr_lut
-    return Spec(L, k, V, int(code)), None
-
-
 def _check_args(sequences, codebook, L, k, V, preds, succs):
-    # Same conditions as forward_backward.py:206-207, plus table shapes.
+    # Same conditions as forward_backward.py:206-207, plus table shapes and devices.
     if not (sequences.dim() == 3 and sequences.shape[-1] == V):
         raise AssertionError(f"sequences must be (B, N, V={V}); got {tuple(sequences.shape)}")
     if tuple(codebook.shape) != (1 << L, V):
@@ -65,32 +70,111 @@ def _check_args(sequences, codebook, L, k, V, preds, succs):
     if not sequences.is_cuda:
         raise AssertionError("bcjr_forward_backward runs on the GPU; sequences are on "
                              f"{sequences.device}")
+    if codebook.device != sequences.device:
+        raise AssertionError(f"codebook is on {codebook.device} but the sequences are on {sequences.device}")
 
 
-class BcjrFunction(torch.autograd.Function):
-    """One autograd node: forward = bcjr_forward, backward = bcjr_backward.
+def temperature_tensor(T, device: torch.device) -> Tensor:
+    """T as a float32 device tensor: (1,) for one value, (B,) for one per sequence.
+    A python number is written by a fill kernel (no host-to-device copy)."""
+    if torch.is_tensor(T):
+        t = T.detach()
+        if t.device != device and t.numel() == 1 and t.device.type == "cpu":
+            return torch.full((1,), float(t), dtype=torch.float32, device=device)
+        return t.to(device=device, dtype=torch.float32).reshape(-1)
+    return torch.full((1,), float(T), dtype=torch.float32, device=device)
 
-    Saves only (sequences, T, table); the backward recomputes the recursions
-    on the GPU (the O(B*N*S) lattice never exists in memory)."""
+
+def _check_T(T: Tensor, B: int):
+    if T.numel() not in (1, B):
+        raise AssertionError(f"T has {T.numel()} values; expected 1 or B={B}")
+
+
+# ---------------------------------------------------------------------------
+# Registered operators
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("bcjr::forward", mutates_args=())
+def bcjr_forward_op(sequences: Tensor, codebook: Tensor, T: Tensor, L: int, k: int,
+                    V: int) -> tuple[Tensor, Tensor]:
+    """soft (B, N, V) and log Z (B,), float32 (bcjr_forward)."""
+    _check_T(T, sequences.shape[0])
+    spec, table = resolve_codebook(codebook, L, k, V, sequences.device)
+    return ops.forward(spec, sequences, T, table)
+
+
+@bcjr_forward_op.register_fake
+def _(sequences, codebook, T, L, k, V):
+    B, N, Vs = sequences.shape
+    return (sequences.new_empty((B, N, Vs), dtype=torch.float32),
+            sequences.new_empty((B,), dtype=torch.float32))
+
+
+@torch.library.custom_op("bcjr::backward", mutates_args=())
+def bcjr_backward_op(sequences: Tensor, codebook: Tensor, T: Tensor, g_soft: Tensor,
+                     g_logZ: Optional[Tensor], L: int, k: int, V: int) -> Tensor:
+    """d sequences (B, N, V) float32 of sum(g_soft * soft) + sum(g_logZ * logZ)
+    (bcjr_backward)."""
+    _check_T(T, sequences.shape[0])
+    spec, table = resolve_codebook(codebook, L, k, V, sequences.device)
+    return ops.backward(spec, sequences, T, table, g_soft, g_logZ)
+
+
+@bcjr_backward_op.register_fake
+def _(sequences, codebook, T, g_soft, g_logZ, L, k, V):
+    return torch.empty_like(sequences, dtype=torch.float32)
+
+
+def _fwd_setup(ctx, inputs, output):
+    sequences, codebook, T, L, k, V = inputs
+    ctx.save_for_backward(sequences, codebook, T)
+    ctx.lkv = (L, k, V)
+
+
+def _fwd_backward(ctx, g_soft, g_logZ):
+    sequences, codebook, T = ctx.saved_tensors
+    L, k, V = ctx.lkv
+    if g_soft is None:
+        g_soft = torch.zeros_like(sequences)
+    d = bcjr_backward_op(sequences, codebook, T, g_soft.contiguous(), g_logZ, L, k, V)
+    return d, None, None, None, None, None
+
+
+bcjr_forward_op.register_autograd(_fwd_backward, setup_context=_fwd_setup)
+
+
+class BcjrInternalsFunction(torch.autograd.Function):
+    """return_internals=True: soft and log Z on the autograd graph (the
+    reference's eager node returns them differentiable,
+    src/bcjr/forward_backward.py:220-231); P, log alpha and log beta are
+    returned without gradient.  The backward is the node's backward."""
 
     @staticmethod
-    def forward(ctx, sequences, T, table, spec):
-        soft, logZ = ops.forward(spec, sequences, T, table)
-        ctx.spec = spec
-        ctx.in_dtype = sequences.dtype
-        ctx.save_for_backward(sequences, T if torch.is_tensor(T) else None,
-                              table if table is not None else None)
-        ctx.T_value = None if torch.is_tensor(T) else float(T)
-        return soft.to(sequences.dtype), logZ.to(sequences.dtype)
+    def forward(ctx, sequences, codebook, T, L, k, V):
+        spec, table = resolve_codebook(codebook, L, k, V, sequences.device)
+        soft, logZ, P, la, lb = ops.forward_internals(spec, sequences, T, table)
+        ctx.save_for_backward(sequences, codebook, T)
+        ctx.lkv = (L, k, V)
+        ctx.mark_non_differentiable(P, la, lb)
+        return soft, logZ, P, la, lb
 
     @staticmethod
-    def backward(ctx, g_soft, g_logZ):
-        sequences, T_saved, table = ctx.saved_tensors
-        T = T_saved if T_saved is not None else ctx.T_value
-        if g_soft is None and g_logZ is None:
-            return None, None, None, None
-        d = ops.backward(ctx.spec, sequences, T, table, g_soft, g_logZ)
-        return d.to(ctx.in_dtype), None, None, None
+    def backward(ctx, g_soft, g_logZ, gP, gla, glb):
+        sequences, codebook, T = ctx.saved_tensors
+        L, k, V = ctx.lkv
+        if g_soft is None:
+            g_soft = torch.zeros_like(sequences)
+        d = bcjr_backward_op(sequences, codebook, T, g_soft.contiguous(), g_logZ, L, k, V)
+        return d, None, None, None, None, None
+
+
+class BcjrFunction:
+    """The node as one autograd function (forward = bcjr::forward, backward =
+    bcjr::backward): BcjrFunction.apply(sequences, codebook, T, L, k, V)."""
+
+    @staticmethod
+    def apply(sequences, codebook, T, L, k, V):
+        return bcjr_forward_op(sequences, codebook, T, L, k, V)
 
 
 def bcjr_forward_backward(sequences, codebook, T_temp,
@@ -99,27 +183,23 @@ def bcjr_forward_backward(sequences, codebook, T_temp,
     """Full BCJR forward-backward (forward_backward.py:190-232).
 
     sequences: (B, N, V) float, requires_grad allowed.
-    codebook:  (2^L, V) float32 (no gradient).
+    codebook:  (2^L, V) float32 on the sequences' device (no gradient).
     T_temp:    temperature > 0: python float, 0-d tensor, or (B,) tensor (one
                per sequence, for batching several tensors in one call).
 
     Returns (soft (B,N,V), log_Z (B,)), or with return_internals
     (soft, log_Z, P, log_alpha, log_beta) with the last three (B, N, 2^L).
-    Both soft and log_Z are differentiable with respect to sequences.
+    soft and log_Z are differentiable with respect to sequences in both forms.
     """
     _check_args(sequences, codebook, L, k, V, preds, succs)
-    spec, table = _spec_for(codebook, L, k, V)
+    dt = sequences.dtype
+    seq = sequences if dt == torch.float32 else sequences.float()
+    T = temperature_tensor(T_temp, sequences.device)
     if return_internals:
-        soft, logZ, P, la, lb = ops.forward_internals(spec, sequences, T_temp, _as_table(spec, table))
-        dt = sequences.dtype
+        soft, logZ, P, la, lb = BcjrInternalsFunction.apply(seq.contiguous(), codebook, T, L, k, V)
         return soft.to(dt), logZ.to(dt), P, la, lb
-    return BcjrFunction.apply(sequences, T_temp, _as_table(spec, table), spec)
-
-
-def _as_table(spec, table):
-    if table is None:
-        return None
-    return table.detach().to(torch.float32).contiguous()
+    soft, logZ = bcjr_forward_op(seq.contiguous(), codebook, T, L, k, V)
+    return soft.to(dt), logZ.to(dt)
 
 
 def bcjr_forward_backward_monolithic(sequences, codebook, T_temp,
@@ -161,6 +241,7 @@ def reset_mono_graph_cache():
 
 __all__ = [
     "L_BITS", "K_BITS", "V_DIM", "build_pred_succ_tables", "bcjr_forward_backward",
-    "bcjr_forward_backward_monolithic", "BcjrFunction", "bcjr_forward_backward_fast",
-    "bcjr_forward_backward_monolithic_graphed", "reset_mono_graph_cache",
+    "bcjr_forward_backward_monolithic", "BcjrFunction", "BcjrInternalsFunction", "bcjr_forward_backward_fast",
+    "bcjr_forward_backward_monolithic_graphed", "reset_mono_graph_cache", "bcjr_forward_op",
+    "bcjr_backward_op", "temperature_tensor",
 ]

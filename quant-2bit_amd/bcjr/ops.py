@@ -47,33 +47,27 @@ def _workspace(prob: _lib.Problem, op: int, device: torch.device) -> torch.Tenso
     return torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=device)
 
 
-_T_CACHE: dict = {}
-
-
-def _scalar_T(value: float, device: torch.device) -> torch.Tensor:
-    """Device copy of a python-float temperature, made once per (device, value), so
-    steady-state calls (and calls under graph capture) do no host-to-device copy."""
-    key = (str(device), float(value))
-    t = _T_CACHE.get(key)
-    if t is None:
-        if len(_T_CACHE) > 256:
-            _T_CACHE.clear()
-        t = torch.tensor([float(value)], dtype=torch.float32, device=device)
-        _T_CACHE[key] = t
-    return t
-
-
 def _temperature(T, B: int, device: torch.device):
-    """float32 device tensor holding one T, or B of them; returns (tensor, per_seq)."""
+    """float32 device tensor holding one T, or B of them; returns (tensor, per_seq).
+    A python number is written by a fill kernel: no host-to-device copy, so the
+    call can be captured into a graph."""
     if torch.is_tensor(T):
         Tt = T.detach().to(device=device, dtype=torch.float32).reshape(-1).contiguous()
     else:
-        Tt = _scalar_T(T, device)
+        Tt = torch.full((1,), float(T), dtype=torch.float32, device=device)
     if Tt.numel() == 1:
         return Tt, False
     if Tt.numel() != B:
         raise AssertionError(f"T has {Tt.numel()} values; expected 1 or B={B}")
     return Tt, True
+
+
+def _on(dev: torch.device, **tensors) -> None:
+    """AssertionError unless every given tensor (None allowed) is on `dev`: the
+    kernels dereference these pointers on that device."""
+    for name, t in tensors.items():
+        if t is not None and t.device != dev:
+            raise AssertionError(f"{name} is on {t.device} but the launch runs on {dev}")
 
 
 def _table(spec: Spec, codebook):
@@ -90,6 +84,7 @@ def forward(spec: Spec, seq: torch.Tensor, T, table: torch.Tensor | None):
     with torch.cuda.device(seq.device):
         seq = seq.detach().to(torch.float32).contiguous()
         B, N, V = seq.shape
+        _on(seq.device, codebook_or_lut=table)
         Tt, per = _temperature(T, B, seq.device)
         soft = torch.empty_like(seq)
         logZ = torch.empty((B,), dtype=torch.float32, device=seq.device)
@@ -108,6 +103,7 @@ def forward_internals(spec: Spec, seq: torch.Tensor, T, table: torch.Tensor | No
     with torch.cuda.device(seq.device):
         seq = seq.detach().to(torch.float32).contiguous()
         B, N, V = seq.shape
+        _on(seq.device, codebook_or_lut=table)
         Tt, per = _temperature(T, B, seq.device)
         soft = torch.empty_like(seq)
         logZ = torch.empty((B,), dtype=torch.float32, device=seq.device)
@@ -130,6 +126,7 @@ def forward_entropy(spec: Spec, seq: torch.Tensor, T, table: torch.Tensor | None
     with torch.cuda.device(seq.device):
         seq = seq.detach().to(torch.float32).contiguous()
         B, N, V = seq.shape
+        _on(seq.device, codebook_or_lut=table)
         Tt, per = _temperature(T, B, seq.device)
         soft = torch.empty_like(seq)
         logZ = torch.empty((B,), dtype=torch.float32, device=seq.device)
@@ -149,6 +146,9 @@ def backward(spec: Spec, seq: torch.Tensor, T, table, g_soft, g_logZ=None):
     with torch.cuda.device(seq.device):
         seq = seq.detach().to(torch.float32).contiguous()
         B, N, V = seq.shape
+        _on(seq.device, codebook_or_lut=table, g_soft=g_soft)
+        if g_soft is not None and tuple(g_soft.shape) != (B, N, V):
+            raise AssertionError(f"g_soft must be {(B, N, V)}; got {tuple(g_soft.shape)}")
         Tt, per = _temperature(T, B, seq.device)
         g = g_soft.detach().to(torch.float32).contiguous() if g_soft is not None else torch.zeros_like(seq)
         gz = None
@@ -176,6 +176,7 @@ def viterbi(spec: Spec, seq: torch.Tensor, table, want_packed: bool = True, over
         seq = seq.detach().to(torch.float32).contiguous()
         B, N, V = seq.shape
         dev = seq.device
+        _on(dev, codebook_or_lut=table)
         out = {
             "walk": torch.empty((B, N), dtype=torch.int32, device=dev),
             "bitstream": torch.empty((B, N), dtype=torch.int32, device=dev),
@@ -212,6 +213,7 @@ def viterbi(spec: Spec, seq: torch.Tensor, table, want_packed: bool = True, over
 def decode(spec: Spec, start: torch.Tensor, table, bitstream=None, packed=None, N: int | None = None):
     """Replay walks; returns (walk (B,N) int32, recon (B,N,V) float32)."""
     dev = start.device
+    _on(dev, codebook_or_lut=table, bitstream=bitstream, packed=packed)
     with torch.cuda.device(dev):
         start = start.to(torch.int32).contiguous()
         B = start.shape[0]
@@ -239,6 +241,7 @@ def decode_walks(spec: Spec, start: torch.Tensor, bitstream: torch.Tensor) -> to
     """Walks only: (B, N) int32 states replayed from start (B,) and a (B, N)
     bitstream; needs no codebook."""
     dev = start.device
+    _on(dev, bitstream=bitstream)
     with torch.cuda.device(dev):
         start = start.to(torch.int32).contiguous()
         bitstream = bitstream.to(torch.int32).contiguous()
@@ -261,6 +264,7 @@ def dequant(spec: Spec, start: torch.Tensor, table, m: int, n: int, Tx: int, Ty:
     """(m, n) float32 matrix scale * c(walk) of Tx x Ty tiles, tile b = col_block *
     (m // Tx) + row_block, from a (B, N) uint8 / int32 bitstream or a packed one."""
     dev = start.device
+    _on(dev, codebook_or_lut=table, bitstream=bitstream, packed=packed)
     with torch.cuda.device(dev):
         start = start.reshape(-1).to(torch.int32).contiguous()
         B = start.shape[0]

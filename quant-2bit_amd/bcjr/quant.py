@@ -57,25 +57,19 @@ def reset_graph_cache():
 def bcjr_quantize_tiles(sequences, codebook, T_temp, preds=None, succs=None,
                         chunk_size=BCJR_CHUNK, use_checkpoint=True,
                         L=L_BITS, k=K_BITS, V=V_DIM):
-    """(B, N, V) -> soft (B, N, V), optionally in chunks (bcjr_quant.py:85-122).
+    """(B, N, V) -> soft (B, N, V) (bcjr_quant.py:85-122).
 
-    The node keeps only its inputs for backward and recomputes on the GPU, so
-    activation checkpointing would only repeat the forward; use_checkpoint is
-    accepted for signature compatibility and not applied."""
-    B = sequences.shape[0]
-    if chunk_size is None or chunk_size >= B:
-        soft, _ = bcjr_forward_backward(sequences, codebook, T_temp, L=L, k=k, V=V,
-                                        preds=preds, succs=succs)
-        return soft
-    outs = []
-    for i in range(0, B, chunk_size):
-        Ti = T_temp
-        if torch.is_tensor(T_temp) and T_temp.numel() == B:
-            Ti = T_temp[i:i + chunk_size]
-        soft, _ = bcjr_forward_backward(sequences[i:i + chunk_size], codebook, Ti, L=L, k=k, V=V,
-                                        preds=preds, succs=succs)
-        outs.append(soft)
-    return torch.cat(outs, dim=0)
+    The reference splits B into chunks of chunk_size sequences and wraps each in
+    an activation checkpoint to bound the memory of its (B, N, 2^L) lattices.
+    Here one launch per direction covers the whole batch with memory bounded by
+    the engine's workspace, and the node keeps only its inputs for the backward,
+    so chunk_size and use_checkpoint are accepted for signature compatibility
+    and not applied: the result is the same (sequences are independent) and a
+    chunked loop would only multiply launches (a 237,568-tile layer at
+    chunk_size=8 would be ~30,000 of them, each filling 8 of 256 CUs)."""
+    soft, _ = bcjr_forward_backward(sequences, codebook, T_temp, L=L, k=k, V=V,
+                                    preds=preds, succs=succs)
+    return soft
 
 
 def bcjr_quantize_weight_rotated(W_rotated, codebook, T_temp, preds=None, succs=None,

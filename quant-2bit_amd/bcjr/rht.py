@@ -47,20 +47,31 @@ def _hadamard(x: torch.Tensor, scale: float) -> torch.Tensor:
     return out
 
 
-class HadamardFunction(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, scale):
-        ctx.scale = scale
-        return _hadamard(x, scale)
+@torch.library.custom_op("bcjr::hadamard", mutates_args=())
+def hadamard_op(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """scale * H_n x along the last axis (bcjr_hadamard)."""
+    return _hadamard(x, scale)
 
-    @staticmethod
-    def backward(ctx, g):  # H is symmetric
-        return _hadamard(g, ctx.scale), None
+
+@hadamard_op.register_fake
+def _(x, scale):
+    return torch.empty(x.shape, dtype=torch.float32, device=x.device)
+
+
+def _hadamard_setup(ctx, inputs, output):
+    ctx.scale = inputs[1]
+
+
+def _hadamard_backward(ctx, g):  # H is symmetric
+    return hadamard_op(g.contiguous(), ctx.scale), None
+
+
+hadamard_op.register_autograd(_hadamard_backward, setup_context=_hadamard_setup)
 
 
 def hadamard_transform(x: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
     """scale * H_n x along the last axis (unscaled Sylvester H_n, n a power of two)."""
-    return HadamardFunction.apply(x, scale)
+    return hadamard_op(x, float(scale))
 
 
 def _check_rht_args(W, sign_l, sign_r):
@@ -85,17 +96,31 @@ def _rht(W, sign_l, sign_r, inverse: bool) -> torch.Tensor:
     return out
 
 
-class RhtFunction(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, W, sign_l, sign_r, inverse):
-        ctx.save_for_backward(sign_l, sign_r)
-        ctx.inverse = inverse
-        return _rht(W, sign_l, sign_r, inverse)
+@torch.library.custom_op("bcjr::rht", mutates_args=())
+def rht_op(W: torch.Tensor, sign_l: torch.Tensor, sign_r: torch.Tensor, inverse: bool) -> torch.Tensor:
+    """The RHT of W (m, n), or its inverse (bcjr_rht)."""
+    return _rht(W, sign_l, sign_r, inverse)
 
-    @staticmethod
-    def backward(ctx, g):  # the adjoint of the transform is its inverse
-        sign_l, sign_r = ctx.saved_tensors
-        return _rht(g.contiguous(), sign_l, sign_r, not ctx.inverse), None, None, None
+
+@rht_op.register_fake
+def _(W, sign_l, sign_r, inverse):
+    if W.dim() != 2 or tuple(sign_l.shape) != (W.shape[0],) or tuple(sign_r.shape) != (W.shape[1],):
+        raise AssertionError(f"RHT of {tuple(W.shape)} with signs {tuple(sign_l.shape)}, {tuple(sign_r.shape)}")
+    return torch.empty(W.shape, dtype=torch.float32, device=W.device)
+
+
+def _rht_setup(ctx, inputs, output):
+    W, sign_l, sign_r, inverse = inputs
+    ctx.save_for_backward(sign_l, sign_r)
+    ctx.inverse = inverse
+
+
+def _rht_backward(ctx, g):  # the adjoint of the transform is its inverse
+    sign_l, sign_r = ctx.saved_tensors
+    return rht_op(g.contiguous(), sign_l, sign_r, not ctx.inverse), None, None, None
+
+
+rht_op.register_autograd(_rht_backward, setup_context=_rht_setup)
 
 
 def _rht_batched(W, sign_l, sign_r, inverse: bool) -> torch.Tensor:
@@ -115,37 +140,48 @@ def _rht_batched(W, sign_l, sign_r, inverse: bool) -> torch.Tensor:
     return out
 
 
-class RhtBatchedFunction(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, W, sign_l, sign_r, inverse):
-        ctx.save_for_backward(sign_l, sign_r)
-        ctx.inverse = inverse
-        return _rht_batched(W, sign_l, sign_r, inverse)
+@torch.library.custom_op("bcjr::rht_batched", mutates_args=())
+def rht_batched_op(W: torch.Tensor, sign_l: torch.Tensor, sign_r: torch.Tensor, inverse: bool) -> torch.Tensor:
+    """The RHT (or its inverse) of each matrix of W (E, m, n) (bcjr_rht_batched)."""
+    return _rht_batched(W, sign_l, sign_r, inverse)
 
-    @staticmethod
-    def backward(ctx, g):
-        sign_l, sign_r = ctx.saved_tensors
-        return _rht_batched(g.contiguous(), sign_l, sign_r, not ctx.inverse), None, None, None
+
+@rht_batched_op.register_fake
+def _(W, sign_l, sign_r, inverse):
+    return torch.empty(W.shape, dtype=torch.float32, device=W.device)
+
+
+def _rht_batched_backward(ctx, g):
+    sign_l, sign_r = ctx.saved_tensors
+    return rht_batched_op(g.contiguous(), sign_l, sign_r, not ctx.inverse), None, None, None
+
+
+rht_batched_op.register_autograd(_rht_batched_backward, setup_context=_rht_setup)
 
 
 def apply_rht_batched(W, sign_l, sign_r):
     """apply_rht_gpu on each matrix of W (E, m, n), signs (E, m) and (E, n)."""
-    return RhtBatchedFunction.apply(W, sign_l, sign_r, False)
+    return rht_batched_op(W, sign_l, sign_r, False)
 
 
 def apply_inverse_rht_batched(W_tilde, sign_l, sign_r):
     """apply_inverse_rht_gpu on each matrix of W_tilde (E, m, n)."""
-    return RhtBatchedFunction.apply(W_tilde, sign_l, sign_r, True)
+    return rht_batched_op(W_tilde, sign_l, sign_r, True)
+
+
+def _as_tensor(v, like):
+    """Sign vector as a tensor (numpy arrays are accepted, as in the reference)."""
+    return v if torch.is_tensor(v) else torch.as_tensor(np.asarray(v, dtype=np.float32), device=like.device)
 
 
 def apply_rht_gpu(W, sign_l_gpu, sign_r_gpu):
     """W~ = H_m diag(sl) W diag(sr) H_n / sqrt(m n)  (src/qat/ste.py:113-126)."""
-    return RhtFunction.apply(W, sign_l_gpu, sign_r_gpu, False)
+    return rht_op(W, _as_tensor(sign_l_gpu, W), _as_tensor(sign_r_gpu, W), False)
 
 
 def apply_inverse_rht_gpu(W_tilde, sign_l_gpu, sign_r_gpu):
     """W = diag(sl) H_m W~ H_n diag(sr) / sqrt(m n)  (src/qat/ste.py:129-135)."""
-    return RhtFunction.apply(W_tilde, sign_l_gpu, sign_r_gpu, True)
+    return rht_op(W_tilde, _as_tensor(sign_l_gpu, W_tilde), _as_tensor(sign_r_gpu, W_tilde), True)
 
 
 __all__ = ["make_sign_vector", "hadamard_transform", "apply_rht_gpu", "apply_inverse_rht_gpu", "apply_rht_batched",

@@ -33,7 +33,7 @@ import numpy as np
 import torch
 
 from . import ops
-from .codes import code_of
+from .codes import resolve_codebook
 from .ops import CODE_HYB, CODE_TABLE, Spec
 from .rht import apply_inverse_rht_gpu
 
@@ -210,14 +210,7 @@ def _codebook_source(L, k, V, codebook=None, decode_fn=None, device="cuda"):
         if res.shape != (1 << L, V):
             raise AssertionError(f"decode_fn returned shape {res.shape}, expected {(1 << L, V)}")
         codebook = torch.from_numpy(np.ascontiguousarray(res, dtype=np.float32)).to(device)
-    if tuple(codebook.shape) != (1 << L, V):
-        raise AssertionError(f"codebook must be {(1 << L, V)}; got {tuple(codebook.shape)}")
-    code = code_of(codebook)
-    if code == CODE_TABLE:
-        return Spec(L, k, V, CODE_TABLE), codebook.detach().to(device=device, dtype=torch.float32).contiguous()
-    if code == CODE_HYB:
-        return Spec(L, k, V, CODE_HYB, int(codebook._bcjr_Q)), codebook._bcjr_lut
-    return Spec(L, k, V, code), None
+    return resolve_codebook(codebook, L, k, V, torch.device(device))
 
 
 def dequant_target_gpu(saved, codebook=None, decode_fn=None, device="cuda", rotated=False):

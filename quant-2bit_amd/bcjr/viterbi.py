@@ -13,7 +13,7 @@ from __future__ import annotations
 import torch
 
 from . import ops
-from .forward_backward import _spec_for
+from .codes import resolve_codebook
 
 
 def viterbi_encode_v_batched_hip(sequences, codebook, L=16, k=2, V=2, return_all=False):
@@ -32,8 +32,7 @@ def viterbi_encode_v_batched_hip(sequences, codebook, L=16, k=2, V=2, return_all
     B, T = sequences.shape
     if T % V != 0:
         raise AssertionError(f"T={T} must be divisible by V={V}")
-    spec, table = _spec_for(codebook, L, k, V)
-    table = None if table is None else table.detach().contiguous()
+    spec, table = resolve_codebook(codebook, L, k, V, sequences.device)
     out = ops.viterbi(spec, sequences.reshape(B, T // V, V), table)
     res = (out["bitstream"], out["start"], out["recon"].reshape(B, T), out["mse"])
     if return_all:
@@ -66,8 +65,7 @@ def viterbi_encode_constrained_v_batched_hip(sequences, codebook, overlap_values
     kV = k * V
     ob = L - kV if overlap_bits is None else int(overlap_bits)
     B, T = sequences.shape
-    spec, table = _spec_for(codebook, L, k, V)
-    table = None if table is None else table.detach().contiguous()
+    spec, table = resolve_codebook(codebook, L, k, V, sequences.device)
     ov = torch.as_tensor(overlap_values, dtype=torch.int64, device=sequences.device).reshape(-1)
     if ov.numel() == 1:
         ov = ov.expand(B)
@@ -88,8 +86,7 @@ def viterbi_encode_tailbiting_v_batched_hip(sequences, codebook, L=16, k=2, V=2,
     kV = k * V
     B, T = sequences.shape
     N = T // V
-    spec, table = _spec_for(codebook, L, k, V)
-    table = None if table is None else table.detach().contiguous()
+    spec, table = resolve_codebook(codebook, L, k, V, sequences.device)
     steps = sequences.reshape(B, N, V)
     rot = ops.viterbi(spec, torch.roll(steps, N // 2, dims=1).contiguous(), table, want_packed=False)
     overlap = (rot["walk"][:, N // 2] >> kV).to(torch.int32)
@@ -124,8 +121,7 @@ def viterbi_encode_chunked(sequences, codebook, chunk=None, L=16, k=2, V=2):
 
 def viterbi_decode_v_batched(bitstreams, start_states, codebook, L=16, k=2, V=2, packed=None, N=None):
     """Replay walks: returns (walks (B, N) int32, recons (B, N*V) float32)."""
-    spec, table = _spec_for(codebook, L, k, V)
-    table = None if table is None else table.detach().contiguous()
+    spec, table = resolve_codebook(codebook, L, k, V, start_states.device)
     walk, recon = ops.decode(spec, start_states, table, bitstream=bitstreams, packed=packed, N=N)
     return walk, recon.reshape(walk.shape[0], -1)
 

@@ -75,6 +75,9 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   double* cvec = reinterpret_cast<double*>(smem + (size_t)8 * NT);  // N  C_{t-1}
   float* wmax = reinterpret_cast<float*>(cvec + ((N + 1) & ~1));    // 2*kMaxWaves
   float* wsum = wmax + 2 * kMaxWaves;                               // 2*kMaxWaves
+  // Last wsum word: the block-wide input flag (at most 8 waves use wsum, launch
+  // bounds 512 threads), 0 outside the check at the start of each sequence.
+  int* bflag = reinterpret_cast<int*>(wsum + kMaxWaves - 1);
   float* wbuf = wsum + 2 * kMaxWaves;                               // N*V
   float* gbuf = wbuf + N * V;                                       // N*V
   float* apart = gbuf + N * V;                                      // 2*nwaves*(V+1) per-wave partials
@@ -130,6 +133,9 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   };
   auto lds_pair = [&](uint32_t off) -> float2& { return *reinterpret_cast<float2*>(smem + off); };
 
+  if (tid == 0) *bflag = 0;
+  __syncthreads();
+
   for (long long b = blockIdx.x; b < P.B; b += gridDim.x) {
     float* slot = P.ws + (size_t)blockIdx.x * (size_t)N * 2 * (size_t)NT;
     const float Tb = P.T[P.t_per_seq ? b : 0];
@@ -150,14 +156,27 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
       }
       gout[t * V + v] = twoT * (a1 - wbuf[t * V + v] * a0);
     };
+    // T must be finite and > 0, the weights and upstream gradients finite;
+    // otherwise the sequence's gradient is NaN.
+    int bad = !(Tb > 0.0f && Tb < INFINITY) || !__builtin_isfinite(gZ);
     for (int i = tid; i < N * V; i += nthr) {
-      wbuf[i] = seqb[i];
-      gbuf[i] = gb[i];
+      const float w = seqb[i], gg = gb[i];
+      wbuf[i] = w;
+      gbuf[i] = gg;
+      bad |= !__builtin_isfinite(w) || !__builtin_isfinite(gg);
     }
     // (m~_{-1}, mu_{-1}) = (log2(R), 0) for every state: what step 0 reads.
     for (int j = tid; j < NT; j += nthr) mm[j] = make_float2((float)KV, 0.0f);
     if (tid < 2 * kMaxWaves) wmax[tid] = -INFINITY;  // waves that do not exist
+    if (bad) *bflag = 1;
     __syncthreads();
+    if (*bflag) {  // uniform: every thread reads the flag after the barrier
+      for (int i = tid; i < N * V; i += nthr) gout[i] = NAN;
+      __syncthreads();
+      if (tid == 0) *bflag = 0;
+      __syncthreads();
+      continue;
+    }
 
     // Below kExactBelowT most groups would underflow the zero-shift sums, so
     // the whole sequence uses the group maxima.  The choice is a uniform branch
@@ -672,6 +691,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 
     // step 0's partials sit in the buffer of the last beta step's parity ((2N - 1) & 1)
     if (tid < V) grad_out(0, 1, tid);
+    if (tid == 0) *bflag = 0;  // every thread read it after the first barrier
     __syncthreads();
   }
 }

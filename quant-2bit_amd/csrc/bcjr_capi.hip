@@ -106,6 +106,33 @@ int validate(const bcjr_problem* p) {
 
 enum { OP_FWD = BCJR_OP_FORWARD, OP_BWD = BCJR_OP_BACKWARD, OP_VIT = BCJR_OP_VITERBI, OP_FWD_INTERNALS = 3 };
 
+// Bytes of one sequence slot of an operation's workspace (a validated problem):
+// forward N * 2^(L-kV) floats (the raw alpha inputs of every step), backward
+// twice that ((m~, mu) pairs), Viterbi one byte of backpointers per reduced
+// state and step.  It depends on the problem only, so an undersized workspace
+// is reported before any device query.
+size_t slot_bytes_of(const bcjr_problem* p, int op) {
+  const size_t NT = (size_t)1 << (p->L - p->k * p->V);
+  size_t b = op == OP_BWD ? (size_t)p->N * 2 * NT * sizeof(float)
+           : op == OP_VIT ? (size_t)p->N * NT
+                          : (size_t)p->N * NT * sizeof(float);
+  return (b + 255) & ~(size_t)255;
+}
+
+// Early argument checks shared by the launching entry points: the problem, then
+// a workspace that holds at least one slot (BCJR_EWORKSPACE).
+int check_ws(const bcjr_problem* p, int op, const void* ws, size_t ws_bytes) {
+  int rc = validate(p);
+  if (rc) return rc;
+  if (p->B == 0) return BCJR_OK;
+  if (!ws) return fail(BCJR_EINVAL, "ws must be non-NULL");
+  const size_t slot = slot_bytes_of(p, op);
+  if (ws_bytes < slot)
+    return fail(BCJR_EWORKSPACE, "workspace of %zu bytes is smaller than one sequence slot (%zu bytes)",
+                ws_bytes, slot);
+  return BCJR_OK;
+}
+
 // Plans depend on (device, op, L, k, V, N, code, Q) only; they are cached so that
 // steady-state calls (and calls made while a stream is being captured into a
 // graph) do no attribute or occupancy queries.
@@ -282,15 +309,14 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
     pl->lds = fwd ? bcjr::fwd_lds_bytes(p->L, KV, p->V, N, nwaves, kcode, p->Q)
                   : bcjr::vit_lds_bytes(p->L, KV, p->V, N, nwaves, vcode, p->Q,
                                         !pl->cache && pl->nthr == 1024);
-    pl->slot_bytes = fwd ? (size_t)N * pl->NT * sizeof(float) : (size_t)N * pl->NT;
+    pl->slot_bytes = slot_bytes_of(p, fwd ? OP_FWD : OP_VIT);
   } else {
     pl->cache = false;
     pl->swz = pick_swizzle(p->L, KV);
     pl->fn = bcjr::bwd_kernel_ptr(KV, p->V, kcode, upt);
     pl->lds = bcjr::bwd_lds_bytes(p->L, KV, p->V, N, nwaves, kcode, p->Q);
-    pl->slot_bytes = (size_t)N * 2 * pl->NT * sizeof(float);
+    pl->slot_bytes = slot_bytes_of(p, OP_BWD);
   }
-  pl->slot_bytes = (pl->slot_bytes + 255) & ~(size_t)255;
   if (!pl->fn)
     return fail(BCJR_EUNSUPPORTED, "no kernel built for L=%d k=%d V=%d code=%d (units/thread %d)",
                 p->L, p->k, p->V, p->code, upt);
@@ -381,6 +407,8 @@ int bcjr_workspace_bytes(const bcjr_problem* prob, int op, size_t* bytes) {
 
 int bcjr_forward(const bcjr_problem* prob, const float* seq, const float* T, const float* codebook_or_lut,
                  float* soft, float* logZ, void* ws, size_t ws_bytes, hipStream_t stream) {
+  int rc0 = check_ws(prob, OP_FWD, ws, ws_bytes);
+  if (rc0 || prob->B == 0) return rc0;
   Plan pl;
   int rc = make_plan(prob, OP_FWD, &pl);
   if (rc) return rc;
@@ -406,6 +434,8 @@ int bcjr_forward(const bcjr_problem* prob, const float* seq, const float* T, con
 int bcjr_forward_internals(const bcjr_problem* prob, const float* seq, const float* T,
                            const float* codebook_or_lut, float* soft, float* logZ, float* marginals,
                            float* log_alpha, float* log_beta, void* ws, size_t ws_bytes, hipStream_t stream) {
+  int rc0 = check_ws(prob, OP_FWD, ws, ws_bytes);
+  if (rc0 || prob->B == 0) return rc0;
   Plan pl;
   int rc = make_plan(prob, OP_FWD_INTERNALS, &pl);
   if (rc) return rc;
@@ -435,6 +465,8 @@ int bcjr_forward_internals(const bcjr_problem* prob, const float* seq, const flo
 int bcjr_forward_entropy(const bcjr_problem* prob, const float* seq, const float* T,
                          const float* codebook_or_lut, float* soft, float* logZ, float* entropy, void* ws,
                          size_t ws_bytes, hipStream_t stream) {
+  int rc0 = check_ws(prob, OP_FWD, ws, ws_bytes);
+  if (rc0 || prob->B == 0) return rc0;
   Plan pl;
   int rc = make_plan(prob, OP_FWD_INTERNALS, &pl);
   if (rc) return rc;
@@ -463,6 +495,8 @@ int bcjr_backward(const bcjr_problem* prob, const float* seq, const float* T, co
                   const float* logZ, const float* g_soft, const float* g_logZ, float* g_seq, void* ws,
                   size_t ws_bytes, hipStream_t stream) {
   (void)logZ;
+  int rc0 = check_ws(prob, OP_BWD, ws, ws_bytes);
+  if (rc0 || prob->B == 0) return rc0;
   Plan pl;
   int rc = make_plan(prob, OP_BWD, &pl);
   if (rc) return rc;
@@ -491,6 +525,8 @@ int bcjr_backward(const bcjr_problem* prob, const float* seq, const float* T, co
 int bcjr_viterbi(const bcjr_problem* prob, const float* seq, const float* codebook_or_lut, int32_t* walk,
                  int32_t* bitstream, int32_t* start_state, float* recon, float* mse, uint8_t* packed, void* ws,
                  size_t ws_bytes, hipStream_t stream) {
+  int rc0 = check_ws(prob, OP_VIT, ws, ws_bytes);
+  if (rc0 || prob->B == 0) return rc0;
   Plan pl;
   int rc = make_plan(prob, OP_VIT, &pl);
   if (rc) return rc;
@@ -520,6 +556,8 @@ int bcjr_viterbi_constrained(const bcjr_problem* prob, const float* seq, const f
                              int overlap_bits, const int32_t* overlap, int32_t* walk, int32_t* bitstream,
                              int32_t* start_state, float* recon, float* mse, uint8_t* packed, void* ws,
                              size_t ws_bytes, hipStream_t stream) {
+  int rc0 = check_ws(prob, OP_VIT, ws, ws_bytes);
+  if (rc0 || prob->B == 0) return rc0;
   Plan pl;
   int rc = make_plan(prob, OP_VIT, &pl);
   if (rc) return rc;

@@ -67,6 +67,9 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   float* mbuf = reinterpret_cast<float*>(cvec + ((N + 1) & ~1));  // 2*NT reduced state (16-B aligned)
   float* wmax = mbuf + 2 * NT;                                    // 2*kMaxWaves
   float* wsum = wmax + 2 * kMaxWaves;                             // kMaxWaves
+  // Last wsum word: the block-wide input flag (at most 8 waves use wsum, launch
+  // bounds 512 threads), 0 outside the check at the start of each sequence.
+  int* bflag = reinterpret_cast<int*>(wsum + kMaxWaves - 1);
   float* wbuf = wsum + kMaxWaves;                                 // N*V   sequence
   // Per-wave partials of the step's soft codeword (V values) and, in the
   // diagnostics variant, of sum_s P log2 P (one more), double-buffered by step.
@@ -109,6 +112,9 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
     }
   }
 
+  if (tid == 0) *bflag = 0;
+  __syncthreads();
+
   for (long long b = blockIdx.x; b < P.B; b += gridDim.x) {
     float* slot = P.ws + (size_t)blockIdx.x * (size_t)N * (size_t)NT;
     const float Tb = P.T[P.t_per_seq ? b : 0];
@@ -123,11 +129,39 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
       for (int w = 0; w < nwaves; ++w) h += spart[(par * nwaves + w) * SP + V];
       P.H_out[(size_t)b * N + t] = -h * (float)kLn2;
     };
-    for (int i = tid; i < N * V; i += nthr) wbuf[i] = seqb[i];
+    // T must be finite and > 0 and the weights finite; otherwise the sequence's
+    // outputs are NaN (the check is one barrier per sequence).
+    int bad = !(Tb > 0.0f && Tb < INFINITY);
+    for (int i = tid; i < N * V; i += nthr) {
+      const float w = seqb[i];
+      wbuf[i] = w;
+      bad |= !__builtin_isfinite(w);
+    }
     // m~_{-1} = log2(R) everywhere: the buffer step 0 reads from.
     for (int j = tid; j < NT; j += nthr) mbuf[NT + j] = (float)KV;
     if (tid < 2 * kMaxWaves) wmax[tid] = -INFINITY;  // waves that do not exist
+    if (bad) *bflag = 1;
     __syncthreads();
+    if (*bflag) {  // uniform: every thread reads the flag after the barrier
+      for (int i = tid; i < N * V; i += nthr) softb[i] = NAN;
+      if (tid == 0 && P.logZ) P.logZ[b] = NAN;
+      if constexpr (INTERNALS) {
+        if (P.H_out)
+          for (int t = tid; t < N; t += nthr) P.H_out[(size_t)b * N + t] = NAN;
+        if (P.P_out) {
+          const size_t per = (size_t)N << L;
+          for (size_t i = tid; i < per; i += nthr) {
+            P.P_out[(size_t)b * per + i] = NAN;
+            P.la_out[(size_t)b * per + i] = NAN;
+            P.lb_out[(size_t)b * per + i] = NAN;
+          }
+        }
+      }
+      __syncthreads();
+      if (tid == 0) *bflag = 0;
+      __syncthreads();
+      continue;
+    }
 
     double logZ2 = 0.0;
     // Below kExactBelowT most groups would underflow the zero-shift sums, so
@@ -583,6 +617,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
     }
     if (INTERNALS && tid == V && P.H_out) entropy_out(0, par0);
     if (tid == 0 && P.logZ) P.logZ[b] = (float)(logZ2 * kLn2);
+    if (tid == 0) *bflag = 0;  // every thread read it after the first barrier
     __syncthreads();
   }
 }

@@ -235,3 +235,94 @@ def test_hyb_column_walk_identity(Q):
     row, col = byte >> 9, (byte >> 3) & 63
     assert row.max() < 32 and (byte & 7).max() == 0
     assert np.array_equal(col + (1 << (Q - 3)) * (row & 15), idx)
+
+
+# ------------------------- contract checks (no device) -------------------------
+
+@pytest.mark.parametrize("op", ["forward", "backward", "viterbi", "viterbi_constrained", "forward_entropy"])
+def test_undersized_workspace_is_reported_before_any_device_call(lib, op):
+    """BCJR_EWORKSPACE through a real call: the slot size depends on the problem
+    alone, so the status comes back on a machine without a GPU.  The pointers
+    are never dereferenced."""
+    import bcjr._lib as BL
+    p = BL.Problem(16, 2, 1, 4, 256, 2, 9, 0)
+    d = ctypes.c_void_p(4096)
+    ws_small = 100
+    if op == "forward":
+        rc = lib.bcjr_forward(ctypes.byref(p), d, d, None, d, None, d, ws_small, None)
+        slot = 256 * (1 << 14) * 4
+    elif op == "forward_entropy":
+        rc = lib.bcjr_forward_entropy(ctypes.byref(p), d, d, None, d, None, d, d, ws_small, None)
+        slot = 256 * (1 << 14) * 4
+    elif op == "backward":
+        rc = lib.bcjr_backward(ctypes.byref(p), d, d, None, None, d, None, d, d, ws_small, None)
+        slot = 256 * (1 << 14) * 8
+    elif op == "viterbi":
+        rc = lib.bcjr_viterbi(ctypes.byref(p), d, None, None, None, None, None, None, None, d, ws_small, None)
+        slot = 256 * (1 << 14)
+    else:
+        rc = lib.bcjr_viterbi_constrained(ctypes.byref(p), d, None, 4, d, None, None, None, None, None, None,
+                                          d, ws_small, None)
+        slot = 256 * (1 << 14)
+    assert rc == BL.BCJR_EWORKSPACE
+    msg = lib.bcjr_last_error().decode()
+    assert f"({slot} bytes)" in msg and "100 bytes" in msg
+
+
+def test_workspace_check_passes_for_empty_batch(lib):
+    import bcjr._lib as BL
+    p = BL.Problem(16, 2, 1, 0, 256, 2, 9, 0)
+    assert lib.bcjr_forward(ctypes.byref(p), None, None, None, None, None, None, 0, None) == 0
+
+
+def test_codebook_device_mismatch_is_an_assertion():
+    """A codebook (or LUT, bitstream, start state) on another device than the
+    launch raises AssertionError before any pointer reaches a kernel."""
+    from bcjr.codes import resolve_codebook
+    from bcjr import ops
+    cb = torch.zeros(1 << 12, 1)
+    with pytest.raises(AssertionError, match="codebook is on cpu"):
+        resolve_codebook(cb, 12, 2, 1, torch.device("cuda:0"))
+    with pytest.raises(AssertionError, match="codebook"):
+        resolve_codebook(torch.zeros(10, 1), 12, 2, 1, torch.device("cuda:0"))
+    with pytest.raises(AssertionError, match="bitstream is on cpu"):
+        ops._on(torch.device("cuda:0"), codebook_or_lut=None, bitstream=torch.zeros(4, dtype=torch.int32))
+    meta = torch.empty(4, device="meta")
+    with pytest.raises(AssertionError, match="packed is on meta"):
+        ops._on(torch.device("cpu"), packed=meta)
+    ops._on(torch.device("cpu"), packed=torch.zeros(2), codebook_or_lut=None)
+
+
+def test_tagged_hyb_lut_device_is_checked():
+    from bcjr.codes import _tag, resolve_codebook
+    cb = _tag(torch.zeros(1 << 8, 2, device="meta"), 3, torch.zeros(1 << 9, 2), 9)
+    with pytest.raises(AssertionError, match="HYB LUT is on cpu"):
+        resolve_codebook(cb, 8, 1, 2, torch.device("meta"))
+
+
+def test_registered_ops_have_fake_implementations():
+    """bcjr::forward / bcjr::backward / bcjr::rht are torch operators whose
+    fake (meta) implementations give the output shapes without a device."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    import bcjr  # noqa: F401  (registers the operators)
+    with FakeTensorMode():
+        seq = torch.empty(5, 32, 1)
+        cb = torch.empty(1 << 8, 1)
+        T = torch.empty(1)
+        soft, logZ = torch.ops.bcjr.forward(seq, cb, T, 8, 2, 1)
+        assert soft.shape == (5, 32, 1) and logZ.shape == (5,) and soft.dtype == torch.float32
+        d = torch.ops.bcjr.backward(seq, cb, T, torch.empty(5, 32, 1), None, 8, 2, 1)
+        assert d.shape == (5, 32, 1)
+        W = torch.empty(64, 32)
+        out = torch.ops.bcjr.rht(W, torch.empty(64), torch.empty(32), False)
+        assert out.shape == (64, 32)
+        h = torch.ops.bcjr.hadamard(torch.empty(3, 16), 0.25)
+        assert h.shape == (3, 16)
+
+
+def test_temperature_tensor_has_no_host_copy_for_python_floats():
+    from bcjr.forward_backward import temperature_tensor
+    t = temperature_tensor(0.25, torch.device("cpu"))
+    assert t.shape == (1,) and t.dtype == torch.float32 and float(t) == 0.25
+    tb = temperature_tensor(torch.tensor([0.1, 0.2], dtype=torch.float64), torch.device("cpu"))
+    assert tb.dtype == torch.float32 and tb.shape == (2,)

@@ -63,7 +63,7 @@ CASES = [
 def test_marginal_entropy_vs_oracle(bcjr_mod, oracle, L, k, V, N, B, kind, T):
     _say(f"entropy L={L} k={k} V={V} N={N} B={B} {kind} T={T}")
     from bcjr import ops
-    from bcjr.forward_backward import _as_table, _spec_for
+    from bcjr.codes import resolve_codebook
     rng = np.random.default_rng(L * 7 + N)
     cb, cb_np = _codebook(bcjr_mod, kind, L, rng)
     seq = rng.standard_normal((B, N, V)).astype(np.float32)
@@ -72,8 +72,8 @@ def test_marginal_entropy_vs_oracle(bcjr_mod, oracle, L, k, V, N, B, kind, T):
     H_ref = oracle.marginal_entropy(seq, cb_np, T, L, k * V)
     assert _h_close(H.cpu().numpy(), H_ref)
     # soft and log Z of the entropy launch are those of the plain forward
-    spec, table = _spec_for(cb, L, k, V)
-    s1, z1, _ = ops.forward_entropy(spec, torch.tensor(seq, device="cuda"), T, _as_table(spec, table))
+    spec, table = resolve_codebook(cb, L, k, V, torch.device("cuda"))
+    s1, z1, _ = ops.forward_entropy(spec, torch.tensor(seq, device="cuda"), T, table)
     s_ref, z_ref = oracle.bcjr_forward(seq, cb_np, T, L, k * V)
     assert max_rel(s1.cpu().numpy(), s_ref) < 1e-4
     assert np.abs(z1.cpu().numpy() - z_ref).max() <= 1e-5 * np.abs(z_ref).max()

@@ -242,7 +242,7 @@ def test_longest_sequences_and_lds_limit(bcjr_mod, oracle):
     L = 16
     cb = make_3inst_codebook(L, "cuda")
     cb_np = cb.cpu().numpy()
-    spec, _ = bcjr_mod.forward_backward._spec_for(cb, L, 2, 1)
+    spec, _ = bcjr_mod.codes.resolve_codebook(cb, L, 2, 1, torch.device("cuda"))
     rng = np.random.default_rng(11)
     seq = rng.standard_normal((1, 2024, 1)).astype(np.float32)
     g = rng.standard_normal((1, 2024, 1)).astype(np.float32)
