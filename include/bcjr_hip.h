@@ -122,6 +122,24 @@ int bcjr_forward_entropy(const bcjr_problem* prob, const float* seq, const float
                          const float* codebook_or_lut, float* soft, float* logZ, float* entropy,
                          void* ws, size_t ws_bytes, hipStream_t stream);
 
+/* bcjr_forward without a workspace argument: it allocates nothing.  No
+ * counterpart in the reference; it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The sequence slots live in a static device array of
+ * BCJR_NOALLOC_SCRATCH_BYTES (128 MiB) that the library holds on every GPU it
+ * runs on until the process ends; as many sequences are in flight as slots fit
+ * (8 at L=16, kV=2, N=256), so its throughput is below bcjr_forward's.  A
+ * problem whose one slot (N * 2^(L-kV) * 4 bytes) exceeds the array returns
+ * BCJR_EWORKSPACE.  Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race and must be
+ * serialised by the caller.  The first call on a device looks up the array's
+ * address (hipGetSymbolAddress) and the launch plan; make it before a
+ * capture begins. */
+#define BCJR_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+int bcjr_forward_noalloc(const bcjr_problem* prob, const float* seq, const float* T,
+                         const float* codebook_or_lut, float* soft, float* logZ,
+                         hipStream_t stream);
+
 /* Gradient of sum(g_soft * soft) + sum(g_logZ * logZ) with respect to the
  * sequences, (B, N, V).  g_logZ may be NULL (treated as zero).  logZ is unused
  * (recomputed) and may be NULL.  Codebook and T get no gradient, as in

@@ -19,7 +19,7 @@ BCJR_OK, BCJR_EINVAL, BCJR_EUNSUPPORTED, BCJR_EWORKSPACE, BCJR_EHIP = 0, -1, -2,
 
 # Every function include/bcjr_hip.h declares.
 EXPORTS = (
-    "bcjr_workspace_bytes", "bcjr_forward", "bcjr_forward_internals", "bcjr_forward_entropy", "bcjr_backward",
+    "bcjr_workspace_bytes", "bcjr_forward", "bcjr_forward_noalloc", "bcjr_forward_internals", "bcjr_forward_entropy", "bcjr_backward",
     "bcjr_viterbi", "bcjr_viterbi_constrained", "bcjr_decode", "bcjr_dequant", "bcjr_codebook", "bcjr_hadamard", "bcjr_rht", "bcjr_rht_batched",
     "bcjr_strerror", "bcjr_last_error", "bcjr_version",
 )
@@ -58,6 +58,7 @@ def load(path: str = LIB_PATH):
     pp = ctypes.POINTER(Problem)
     lib.bcjr_workspace_bytes.argtypes = [pp, i32, ctypes.POINTER(sz)]
     lib.bcjr_forward.argtypes = [pp, vp, vp, vp, vp, vp, vp, sz, vp]
+    lib.bcjr_forward_noalloc.argtypes = [pp, vp, vp, vp, vp, vp, vp]
     lib.bcjr_forward_internals.argtypes = [pp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.bcjr_forward_entropy.argtypes = [pp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.bcjr_backward.argtypes = [pp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
@@ -71,7 +72,7 @@ def load(path: str = LIB_PATH):
     lib.bcjr_rht_batched.argtypes = [vp, vp, i64, i64, i64, vp, vp, i32, vp]
     lib.bcjr_dequant.argtypes = [pp, vp, i32, vp, vp, i64, i64, i32, i32, ctypes.c_double, vp, vp]
     lib.bcjr_strerror.argtypes = [i32]
-    for name in ("bcjr_workspace_bytes", "bcjr_forward", "bcjr_forward_internals", "bcjr_forward_entropy",
+    for name in ("bcjr_workspace_bytes", "bcjr_forward", "bcjr_forward_noalloc", "bcjr_forward_internals", "bcjr_forward_entropy",
                  "bcjr_backward", "bcjr_viterbi", "bcjr_viterbi_constrained", "bcjr_decode", "bcjr_dequant", "bcjr_codebook", "bcjr_hadamard", "bcjr_rht", "bcjr_rht_batched"):
         getattr(lib, name).restype = i32
     for name in ("bcjr_strerror", "bcjr_last_error", "bcjr_version"):

@@ -350,7 +350,33 @@ int launch(const Plan& pl, long long B, size_t ws_bytes, void* params, hipStream
 
 }  // namespace
 
+// Sequence slots of bcjr_forward_noalloc: a static device array, one copy per
+// GPU.  Host code never names it after set-up: its host-side symbol is only a
+// stand-in, so the device address comes from hipGetSymbolAddress, once per
+// device with that device current, and is kept per device.
+static __device__ __align__(256) unsigned char scratch[BCJR_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];
+
+int scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= 64) return fail(BCJR_EHIP, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(BCJR_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return BCJR_OK;
+}
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -429,6 +455,21 @@ int bcjr_forward(const bcjr_problem* prob, const float* seq, const float* T, con
   P.Q = prob->Q;
   P.t_per_seq = prob->t_per_seq ? 1 : 0;
   return launch(pl, prob->B, ws_bytes, &P, stream);
+}
+
+int bcjr_forward_noalloc(const bcjr_problem* prob, const float* seq, const float* T, const float* codebook_or_lut,
+                         float* soft, float* logZ, hipStream_t stream) {
+  int rc = validate(prob);
+  if (rc || prob->B == 0) return rc;
+  const size_t slot = slot_bytes_of(prob, OP_FWD);
+  if (slot > BCJR_NOALLOC_SCRATCH_BYTES)
+    return fail(BCJR_EWORKSPACE,
+                "one sequence slot needs %zu bytes (N=%lld, L=%d, k*V=%d); the static scratch holds %zu",
+                slot, (long long)prob->N, prob->L, prob->k * prob->V, (size_t)BCJR_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = scratch_ptr(&ws);
+  if (rc) return rc;
+  return bcjr_forward(prob, seq, T, codebook_or_lut, soft, logZ, ws, BCJR_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int bcjr_forward_internals(const bcjr_problem* prob, const float* seq, const float* T,
