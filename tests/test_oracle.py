@@ -338,3 +338,27 @@ def test_rht_matches_matrix_form_and_inverts(oracle, m, n):
     back = oracle.inverse_rht(Wt, sl, sr)
     assert np.abs(back - W).max() <= 1e-5 * np.abs(W).max()
     assert abs(np.linalg.norm(Wt) - np.linalg.norm(W)) <= 1e-5 * np.linalg.norm(W)  # orthogonal
+
+
+def test_torch_eager_restatement_matches_oracle(oracle):
+    """oracle/torch_ref.py (the reference's eager node in torch float32, the CPU
+    baseline of bench.py) against the float64 C oracle: soft, log Z and the
+    gradient, V = 1 and V = 2, with and without the per-step checkpoint."""
+    import torch
+    from oracle.torch_ref import eager_bcjr, eager_step
+    for L, kV, V, code in ((8, 2, 1, oracle.CODE_1MAD), (8, 4, 2, None)):
+        rng = np.random.default_rng(L + kV)
+        B, N = 3, 24
+        seq = rng.standard_normal((B, N, V)).astype(np.float32)
+        g = rng.standard_normal((B, N, V)).astype(np.float32)
+        cb = oracle.codebook(code, L) if code else rng.standard_normal((1 << L, V)).astype(np.float32)
+        s, z, d = eager_step(torch.tensor(seq), torch.tensor(cb), 0.2, L, kV, torch.tensor(g))
+        s_ref, z_ref = oracle.bcjr_forward(seq, cb, 0.2, L, kV)
+        d_ref = oracle.bcjr_backward(seq, cb, 0.2, L, kV, g)
+        assert np.abs(s.numpy() - s_ref).max() <= 1e-4 * np.abs(s_ref).max()
+        assert np.abs(z.numpy() - z_ref).max() <= 1e-5 * np.abs(z_ref).max()
+        assert np.abs(d.numpy() - d_ref).max() <= 1e-3 * np.abs(d_ref).max()
+        x = torch.tensor(seq, requires_grad=True)
+        s2, _ = eager_bcjr(x, torch.tensor(cb), 0.2, L, kV, checkpoint=False)
+        s2.backward(torch.tensor(g))
+        assert torch.allclose(s2.detach(), s, rtol=0, atol=1e-6) and torch.allclose(x.grad, d, rtol=0, atol=1e-5)
