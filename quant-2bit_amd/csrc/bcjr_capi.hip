@@ -309,6 +309,17 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
     pl->lds = fwd ? bcjr::fwd_lds_bytes(p->L, KV, p->V, N, nwaves, kcode, p->Q)
                   : bcjr::vit_lds_bytes(p->L, KV, p->V, N, nwaves, vcode, p->Q,
                                         !pl->cache && pl->nthr == 1024);
+    if (op == OP_FWD && KV == 2 && p->V == 1 && p->L >= 14 && p->code <= BCJR_CODE_3INST) {
+      // Four waves per SIMD: 1024 threads, every codeword in VGPRs (bcjr_fwd4.hip).
+      const int upt4 = 1 << (p->L - 14);
+      const void* fn4 = bcjr::fwd4_kernel_ptr(p->code, upt4);
+      if (fn4) {
+        pl->fn = fn4;
+        pl->nthr = nthr = 1024;
+        pl->upt = upt4;
+        pl->lds = bcjr::fwd4_lds_bytes(p->L, N);
+      }
+    }
     pl->slot_bytes = slot_bytes_of(p, fwd ? OP_FWD : OP_VIT);
   } else {
     pl->cache = false;

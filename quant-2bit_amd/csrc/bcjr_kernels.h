@@ -32,6 +32,9 @@ constexpr int bwd_cached_units(int KV, int V, int upt) {
 }
 
 const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool internals);
+// The four-waves-per-SIMD forward (bcjr_fwd4.hip): kV = 2, V = 1, codes TABLE /
+// 1MAD / 3INST, 1024 threads, upt = 2^(L-14) butterflies per thread (L = 14..16).
+const void* fwd4_kernel_ptr(int code, int upt);
 const void* bwd_kernel_ptr(int KV, int V, int code, int upt);
 const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache, bool wide);
 const void* decode_kernel_ptr(int KV, int V, int code);
@@ -66,6 +69,11 @@ inline size_t fwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, i
   if (code == 3) b += 8u + 8u * ((size_t)2 << Q);  // signed LUT, 8-byte aligned
   if (code == 4) b += 8u + 32u * 64u * 8u;         // column-walk LUT (32 rows of 64)
   return b;
+}
+
+inline size_t fwd4_lds_bytes(int L, int N) {
+  const size_t NT = (size_t)1 << (L - 2);
+  return 8u * (size_t)((N + 1) & ~1) + 4u * (2 * NT + 3 * 16 + 4 + (size_t)N + 2 * 16);
 }
 
 inline size_t bwd_lds_bytes(int L, int KV, int V, int N, int nwaves, int code, int Q) {

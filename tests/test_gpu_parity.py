@@ -105,6 +105,10 @@ CASES = [
     (16, 2, 1, 128, 2, "3inst", 0.01),   # the float32 floor the reference states (T >= 1e-2)
     (16, 2, 2, 64, 2, "hyb", 0.1),       # reference QAT trellis (L=16, kV=4)
     (16, 2, 1, 1024, 1, "3inst", 0.1),   # long sequence: per-step partials are double-buffered
+    (16, 2, 1, 128, 2, "table", 0.2),    # table codebook on the 1024-thread forward
+    (14, 2, 1, 64, 3, "1mad", 0.05),     # 1024-thread forward, exact variant, 1 butterfly per thread
+    (15, 2, 1, 64, 2, "3inst", 0.07),    # 1024-thread forward, exact variant, 2 per thread
+    (15, 2, 1, 64, 2, "table", 0.3),
 ]
 
 
@@ -233,7 +237,7 @@ def test_short_and_empty_batches(bcjr_mod, oracle, L, k, V, kind):
 
 def test_longest_sequences_and_lds_limit(bcjr_mod, oracle):
     """Maximum sizes at L=16, V=1 (3INST, T=0.1): the backward's longest
-    sequence (N = 2024) and the forward's (N = 2704) against the oracle, and one
+    sequence (N = 2024) and the forward's (N = 2702) against the oracle, and one
     step more is refused (BcjrError naming the LDS need) before any launch."""
     _say("longest sequences L=16")
     from bcjr import bcjr_forward_backward, make_3inst_codebook
@@ -252,11 +256,11 @@ def test_longest_sequences_and_lds_limit(bcjr_mod, oracle):
     s_ref, z_ref = oracle.bcjr_forward(seq, cb_np, 0.1, L, 2)
     assert max_rel(soft.detach().cpu().numpy(), s_ref) < SOFT_TOL
     assert max_rel(x.grad.cpu().numpy(), oracle.bcjr_backward(seq, cb_np, 0.1, L, 2, g)) < GRAD_TOL
-    seq2 = rng.standard_normal((1, 2704, 1)).astype(np.float32)
+    seq2 = rng.standard_normal((1, 2702, 1)).astype(np.float32)
     soft2, _ = ops.forward(spec, torch.tensor(seq2, device="cuda"), 0.1, None)
     assert max_rel(soft2.cpu().numpy(), oracle.bcjr_forward(seq2, cb_np, 0.1, L, 2)[0]) < SOFT_TOL
     with pytest.raises(BcjrError, match="LDS"):
-        ops.forward(spec, torch.zeros((1, 2705, 1), device="cuda"), 0.1, None)
+        ops.forward(spec, torch.zeros((1, 2703, 1), device="cuda"), 0.1, None)
     with pytest.raises(BcjrError, match="LDS"):
         ops.backward(spec, torch.zeros((1, 2025, 1), device="cuda"), 0.1, None, torch.zeros((1, 2025, 1), device="cuda"))
 
