@@ -306,6 +306,22 @@ __device__ __forceinline__ int opaque(int x) {
   return x;
 }
 
+// The same for a float kept in a VGPR.  The rare underflow recompute of a
+// butterfly derives its exponents from such a copy of -w_t*sk, so they are
+// recomputed there instead of kept live from the fast path across the test.
+__device__ __forceinline__ float opaque_f(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// The fast path's results exist at this point: nothing of it is sunk past the
+// underflow test, so its per-state exponentials are dead at the branch.
+__device__ __forceinline__ void materialise_one(float x) { asm volatile("" ::"v"(x)); }
+template <typename... Ts>
+__device__ __forceinline__ void materialise(Ts... x) {
+  (materialise_one(x), ...);
+}
+
 // Wave-uniform variant.  The LCG kernels keep A*NT behind it so that
 // base + A*(p*NT + c) cannot be refolded into one multiply A*s + B per state.
 __device__ __forceinline__ uint32_t opaque_uniform(uint32_t x) {

@@ -43,19 +43,6 @@ __device__ __forceinline__ double uniform_d(double x) {
 
 __device__ __forceinline__ float max4(const float (&v)[4]) { return fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])); }
 
-// The fast path's four results exist here: nothing of the fast path is sunk past
-// the underflow test, so its 16 exponentials are dead at the branch.
-__device__ __forceinline__ void materialise(float a, float b, float c, float d) {
-  asm volatile("" ::"v"(a), "v"(b), "v"(c), "v"(d));
-}
-
-// x, opaque to the optimiser: the rare recompute path derives its exponents
-// from it, so they are recomputed there instead of kept live from the fast path.
-__device__ __forceinline__ float opaque_f(float x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
 // f(0) ... f(UPT - 1): unrolled, or as a loop (one unit's registers reused).
 template <bool ROLLED, int UPT, typename F>
 __device__ __forceinline__ void for_units(F&& f) {
@@ -356,7 +343,7 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
             }
             const float smin = fminf(fminf(sp[0], sp[1]), fminf(sp[2], sp[3]));
             materialise(no[0], no[1], no[2], no[3]);
-            materialise(ua, smin, ua, smin);
+            materialise(ua, smin);
             if (smin < kUnderflow) {  // redo the butterfly against the group maxima
               const float nwx = opaque_f(nw);
               ua = 0.0f;
