@@ -515,6 +515,7 @@ def main():
 
     if args.config == "tile":
         res = tile_config(torch, bcjr, ops, dev, exp_peak)
+        calibration_copy(torch, dev)
         print(json.dumps({"metric": METRIC, "value": res["state_updates_per_s"], "unit": "state-updates/s",
                           "n_gpus": 1, "steps": 3, "warmup": 1, "ms_per_step": res["fwd_ms"] + res["bwd_ms"],
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
@@ -539,7 +540,7 @@ def main():
     soft_s = fwd_s + bwd_s
     per_cell = trans_per_cell_grad(2)
     traffic = read_traffic()
-    roofline = {"bound": "valu_exp", "kernel": "bcjr_fwd_kernel + bcjr_bwd_kernel (the layer's soft launches)",
+    roofline = {"bound": "valu_exp", "kernel": "bcjr_fwd4_kernel<2,4> + bcjr_bwd_kernel<2,1,2,8,4> (the layer's soft launches)",
                 "achieved": per_cell * cells / soft_s / 1e12, "peak": exp_peak / 1e12, "unit": "Texp/s",
                 "frac": per_cell * cells / soft_s / exp_peak, "traffic": traffic,
                 "per_cell": per_cell, "cells": cells, "launch_s": soft_s,
@@ -547,8 +548,9 @@ def main():
     if traffic is not None:
         roofline["hbm_GB_s"] = traffic / soft_s / 1e9
         roofline["hbm_floor_s"] = traffic / 8e12
+        roofline["hbm_frac"] = traffic / soft_s / 8e12
     kernels = {
-        "bcjr_fwd_kernel": {"s": fwd_s, "trans_per_cell": trans_per_cell_soft(2),
+        "bcjr_fwd4_kernel": {"s": fwd_s, "trans_per_cell": trans_per_cell_soft(2),
                             "frac": trans_per_cell_soft(2) * cells / fwd_s / exp_peak},
         "bcjr_bwd_kernel": {"s": bwd_s, "trans_per_cell": 2.0, "frac": 2.0 * cells / bwd_s / exp_peak},
         "bcjr_viterbi_kernel": {"s": vit_s, "cell_updates_per_s": cells / vit_s},
