@@ -41,7 +41,11 @@
  *     bcjr_strerror() names it and bcjr_last_error() gives the detail of the
  *     calling thread's last failure.  No C++ exception crosses the ABI.
  *   - Temperature T is read from device memory (a 0-d tensor or one value per
- *     sequence when t_per_seq != 0); it must be finite and > 0.
+ *     sequence when t_per_seq != 0); it must be finite and > 0.  The soft
+ *     kernels check this on the device: a sequence whose T is not finite and
+ *     positive, or whose weights (or, for the backward, upstream gradients) are
+ *     not all finite, gets NaN in every output of that sequence (soft and log Z,
+ *     or its gradient); the other sequences of the launch are unaffected.
  *   - Calls on different streams may overlap as long as their `ws` buffers
  *     differ.
  */
