@@ -17,6 +17,8 @@
  *                  with the tie rules of src/viterbi/encode.py:250-307
  *   bcjr_viterbi_constrained  src/viterbi/encode.py:105-172, 328-389
  *                  (viterbi_encode_constrained, _v: the inner pass of tail-biting)
+ *   bcjr_viterbi_trace  src/viterbi/encode.py:250-307 with return_trace=True
+ *                  (trace_err and backpointers of viterbi_encode_v)
  *   bcjr_decode    src/viterbi/encode.py:310-325 (viterbi_decode_v) and
  *                  src/qat/ste.py:270-283 (_replay_walks)
  *   bcjr_dequant   src/quantize/serialize.py:56-107 (dequant_target, before the
@@ -185,6 +187,17 @@ int bcjr_viterbi_constrained(const bcjr_problem* prob, const float* seq, const f
 int bcjr_decode(const bcjr_problem* prob, const int32_t* bitstream, const uint8_t* packed,
                 const int32_t* start_state, const float* codebook_or_lut, int32_t* walk,
                 float* recon, hipStream_t stream);
+
+/* The full min-sum lattice of each sequence: trace[b][t][s] = cum_t(s), the
+ * cumulative cost of state s after step t, and backptr[b][t][s] = the
+ * predecessor state its minimum chose (the lowest on a tie), with the float32
+ * rounding of bcjr_viterbi.  trace (B, N, 2^L) float32, backptr (B, N, 2^L)
+ * int32, both caller-owned (2^L * N * 8 bytes per sequence: 128 MiB at L = 16,
+ * N = 256).  A diagnostic; needs no workspace.
+ * Replaces the return_trace=True outputs of viterbi_encode_v
+ * (src/viterbi/encode.py:250-307: trace_err, backpointers). */
+int bcjr_viterbi_trace(const bcjr_problem* prob, const float* seq, const float* codebook_or_lut,
+                       float* trace, int32_t* backptr, hipStream_t stream);
 
 /* Bitstream layouts accepted by bcjr_dequant. */
 enum {

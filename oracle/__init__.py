@@ -19,6 +19,8 @@ Contents
                           covariance of the codeword sequence), plus the
                           min-cost path.  Pins the recursions independently of
                           their form.
+``viterbi_trace``         numpy restatement of the encoder's return_trace=True
+                          lattices (src/viterbi/encode.py:250-307).
 ``pack_bits / unpack_bits``
                           2-bit (k*V-bit) LSB-first packing of per-step indices.
 ``fwht / rht / inverse_rht``
@@ -35,6 +37,11 @@ bcjr_forward / bcjr_backward   brute-force path enumeration on tiny trellises (i
                                linearity of the gradient in g.
 marginal_entropy               -sum P ln P of naive_forward's P; L ln 2 at T -> inf;
                                -> 0 at T -> 0 with a unique minimum.
+viterbi_trace                  bit-exact against the float32 prefix costs of every
+                               path (brute force: cum_t(s) is the smallest prefix cost
+                               of the paths through s at t, and the backpointer the
+                               lowest predecessor attaining it); its backtrace equals
+                               the C encoder's walk and start.
 viterbi / decode               the L=2 known answer of the reference's
                                test_viterbi.py:17-53, brute-force minimum-cost paths,
                                tie rules, the 1MAD Table-1 MSE band, round trips;
@@ -218,6 +225,33 @@ def viterbi_tailbiting(seq, cb, L, k, V, nthreads: int = 0):
     walk_r, _, _, _, _ = viterbi(np.roll(seq, N // 2, axis=1), cb, L, kV, nthreads)
     overlap = (walk_r[:, N // 2] >> kV).astype(np.int32)
     return viterbi(seq, cb, L, kV, nthreads, overlap=overlap, overlap_bits=L - kV) + (overlap,)
+
+
+def viterbi_trace(seq1, cb, L, KV):
+    """The return_trace=True lattices of viterbi_encode_v for ONE sequence (N, V)
+    (src/viterbi/encode.py:250-307), in numpy float32: trace[t, s] = cum_t(s),
+    backptr[t, s] = the predecessor its minimum chose.  Predecessors of s are
+    (p << (L - kV)) | (s >> kV), p ascending (encode.py:218-230); the first
+    minimum wins; cum_{-1} = 0; the local cost is sum_v (c_v - w_v)^2 in float32."""
+    x = np.asarray(seq1, np.float32)
+    cb = np.asarray(cb, np.float32)
+    S, R = 1 << L, 1 << KV
+    states = np.arange(S, dtype=np.int64)
+    pred = (np.arange(R, dtype=np.int64)[None, :] << (L - KV)) | (states[:, None] >> KV)  # (S, R)
+    cum = np.zeros(S, np.float32)
+    trace = np.empty((x.shape[0], S), np.float32)
+    backptr = np.empty((x.shape[0], S), np.int32)
+    for t in range(x.shape[0]):
+        diff = cb - x[t][None, :]
+        local = np.zeros(S, np.float32)
+        for v in range(cb.shape[1]):
+            local = local + diff[:, v] * diff[:, v]
+        cand = cum[pred]                          # (S, R) costs of the predecessors
+        first = np.argmin(cand, axis=1)           # lowest p among the minima
+        cum = cand[states, first] + local
+        trace[t] = cum
+        backptr[t] = pred[states, first]
+    return trace, backptr
 
 
 def decode(bitstream, start, cb, L, KV):

@@ -20,7 +20,7 @@ BCJR_OK, BCJR_EINVAL, BCJR_EUNSUPPORTED, BCJR_EWORKSPACE, BCJR_EHIP = 0, -1, -2,
 # Every function include/bcjr_hip.h declares.
 EXPORTS = (
     "bcjr_workspace_bytes", "bcjr_forward", "bcjr_forward_noalloc", "bcjr_forward_internals", "bcjr_forward_entropy", "bcjr_backward",
-    "bcjr_viterbi", "bcjr_viterbi_constrained", "bcjr_decode", "bcjr_dequant", "bcjr_codebook", "bcjr_hadamard", "bcjr_rht", "bcjr_rht_batched",
+    "bcjr_viterbi", "bcjr_viterbi_constrained", "bcjr_viterbi_trace", "bcjr_decode", "bcjr_dequant", "bcjr_codebook", "bcjr_hadamard", "bcjr_rht", "bcjr_rht_batched",
     "bcjr_strerror", "bcjr_last_error", "bcjr_version",
 )
 
@@ -65,6 +65,7 @@ def load(path: str = LIB_PATH):
     lib.bcjr_viterbi.argtypes = [pp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.bcjr_viterbi_constrained.argtypes = [pp, vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.bcjr_decode.argtypes = [pp, vp, vp, vp, vp, vp, vp, vp]
+    lib.bcjr_viterbi_trace.argtypes = [pp, vp, vp, vp, vp, vp]
     lib.bcjr_codebook.argtypes = [pp, vp, vp, vp]
     i64 = ctypes.c_int64
     lib.bcjr_hadamard.argtypes = [vp, vp, i64, i64, ctypes.c_float, vp]
@@ -73,7 +74,7 @@ def load(path: str = LIB_PATH):
     lib.bcjr_dequant.argtypes = [pp, vp, i32, vp, vp, i64, i64, i32, i32, ctypes.c_double, vp, vp]
     lib.bcjr_strerror.argtypes = [i32]
     for name in ("bcjr_workspace_bytes", "bcjr_forward", "bcjr_forward_noalloc", "bcjr_forward_internals", "bcjr_forward_entropy",
-                 "bcjr_backward", "bcjr_viterbi", "bcjr_viterbi_constrained", "bcjr_decode", "bcjr_dequant", "bcjr_codebook", "bcjr_hadamard", "bcjr_rht", "bcjr_rht_batched"):
+                 "bcjr_backward", "bcjr_viterbi", "bcjr_viterbi_constrained", "bcjr_viterbi_trace", "bcjr_decode", "bcjr_dequant", "bcjr_codebook", "bcjr_hadamard", "bcjr_rht", "bcjr_rht_batched"):
         getattr(lib, name).restype = i32
     for name in ("bcjr_strerror", "bcjr_last_error", "bcjr_version"):
         getattr(lib, name).restype = ctypes.c_char_p

@@ -14,14 +14,16 @@ reference computes it.
 
 viterbi_encode_v_batched (encode.py:425-495) returns the same values as
 viterbi_encode_v on each sequence, which is what the reference's own gate asks
-of it (src/tripwires/test_viterbi_batched.py:27-72).  return_trace=True, which
-materialises the (T, 2^L) cost and predecessor lattices, is not provided.
+of it (src/tripwires/test_viterbi_batched.py:27-72).  return_trace=True adds
+the (T/V, 2^L) lattices of cumulative costs and chosen predecessor states, from
+one more launch (bcjr_viterbi_trace) with the same rounding and tie rules.
 """
 from __future__ import annotations
 
 import numpy as np
 import torch
 
+from . import ops
 from .viterbi import (viterbi_decode_v_batched, viterbi_encode_constrained_v_batched_hip,
                       viterbi_encode_tailbiting_v_batched_hip, viterbi_encode_v_batched_hip)
 
@@ -79,15 +81,19 @@ def _mse(recon, sequence):
 
 def viterbi_encode_v(sequence, L, k, V, decode_fn, return_trace=False):
     """(bitstream (T/V,) int32, start_state int, recon (T,) float32, mse float)
-    (encode.py:250-307)."""
-    if return_trace:
-        raise NotImplementedError("return_trace materialises the (T, 2^L) lattices; not provided")
+    (encode.py:250-307); with return_trace=True also trace_err (T/V, 2^L)
+    float32, the cumulative cost of every state after every step, and
+    backpointers (T/V, 2^L) int32, the predecessor each state's minimum chose."""
     x = _sequences(sequence, V)
     cb = _gpu_codebook(L, V, decode_fn)
-    bits, start, recon, _ = viterbi_encode_v_batched_hip(torch.from_numpy(x[None]).to(cb.device), cb,
-                                                         L=L, k=k, V=V)
+    xs = torch.from_numpy(x[None]).to(cb.device)
+    bits, start, recon, _ = viterbi_encode_v_batched_hip(xs, cb, L=L, k=k, V=V)
     recon = recon[0].cpu().numpy()
-    return bits[0].cpu().numpy(), int(start[0]), recon, _mse(recon, np.asarray(sequence))
+    out = (bits[0].cpu().numpy(), int(start[0]), recon, _mse(recon, np.asarray(sequence)))
+    if not return_trace:
+        return out
+    trace, backptr = ops.viterbi_trace(ops.Spec(L, k, V, ops.CODE_TABLE), xs.reshape(1, -1, V), cb)
+    return out + (trace[0].cpu().numpy(), backptr[0].cpu().numpy())
 
 
 def viterbi_encode(sequence, L, k, decode_fn, return_trace=False):

@@ -237,6 +237,30 @@ def decode(spec: Spec, start: torch.Tensor, table, bitstream=None, packed=None, 
         return walk, recon
 
 
+def viterbi_trace(spec: Spec, x: torch.Tensor, table):
+    """The full min-sum lattice of each sequence x (B, N, V): (trace (B, N, 2^L)
+    float32 cumulative costs, backptr (B, N, 2^L) int32 chosen predecessor
+    states), as viterbi_encode_v(..., return_trace=True) returns them for one
+    sequence (src/viterbi/encode.py:250-307)."""
+    dev = x.device
+    _on(dev, codebook_or_lut=table)
+    with torch.cuda.device(dev):
+        x = x.to(torch.float32).contiguous()
+        B, N, V = x.shape
+        if V != spec.V:
+            raise AssertionError(f"sequences have V={V}, spec V={spec.V}")
+        S = 1 << spec.L
+        trace = torch.empty((B, N, S), dtype=torch.float32, device=dev)
+        backptr = torch.empty((B, N, S), dtype=torch.int32, device=dev)
+        if B == 0 or N == 0:
+            return trace, backptr
+        prob = spec.problem(B, N)
+        _lib.check(_lib.load().bcjr_viterbi_trace(
+            ctypes.byref(prob), _lib.ptr(x), _lib.ptr(table), _lib.ptr(trace), _lib.ptr(backptr),
+            _stream(dev)), "bcjr_viterbi_trace")
+        return trace, backptr
+
+
 def decode_walks(spec: Spec, start: torch.Tensor, bitstream: torch.Tensor) -> torch.Tensor:
     """Walks only: (B, N) int32 states replayed from start (B,) and a (B, N)
     bitstream; needs no codebook."""

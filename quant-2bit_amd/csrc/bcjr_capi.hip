@@ -662,6 +662,34 @@ int bcjr_decode(const bcjr_problem* prob, const int32_t* bitstream, const uint8_
   return BCJR_OK;
 }
 
+int bcjr_viterbi_trace(const bcjr_problem* prob, const float* seq, const float* codebook_or_lut, float* trace,
+                       int32_t* backptr, hipStream_t stream) {
+  int rc = validate(prob);
+  if (rc) return rc;
+  if (prob->B == 0) return BCJR_OK;
+  if (!seq || !trace || !backptr) return fail(BCJR_EINVAL, "seq, trace and backptr must be non-NULL");
+  if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
+    return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  const int KV = prob->k * prob->V;
+  const void* fn = bcjr::trace_kernel_ptr(KV, prob->V, prob->code);
+  if (!fn) return fail(BCJR_EUNSUPPORTED, "no trace kernel for k*V=%d V=%d code=%d", KV, prob->V, prob->code);
+  DeviceInfo di;
+  rc = device_info(&di);
+  if (rc) return rc;
+  // The reduced vector and its argmin: NT floats + NT bytes (NT <= 2^14 for a
+  // validated problem, so at most 16 reduced indices per thread of 1024).
+  const int NT = 1 << (prob->L - KV);
+  const int nthr = NT < 64 ? 64 : (NT > 1024 ? 1024 : NT);
+  const size_t lds = (size_t)NT * (sizeof(float) + 1);
+  const long long cap = (long long)di.num_cu * 2;
+  const unsigned grid = (unsigned)(prob->B < cap ? prob->B : cap);
+  bcjr::TraceParams P = {seq, codebook_or_lut, trace, backptr, prob->B, (int)prob->N, prob->L, prob->Q};
+  void* args[] = {&P};
+  hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(nthr), args, lds, stream);
+  if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel(viterbi_trace)");
+  return BCJR_OK;
+}
+
 static_assert(bcjr::BITS_FMT_U8 == BCJR_BITS_U8 && bcjr::BITS_FMT_I32 == BCJR_BITS_I32 &&
                   bcjr::BITS_FMT_PACKED == BCJR_BITS_PACKED,
               "bitstream layout ids");

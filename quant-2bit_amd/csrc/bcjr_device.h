@@ -462,6 +462,15 @@ struct DecParams {
   int N, L, Q;
 };
 
+struct TraceParams {
+  const float* seq;    // (B, N, V)
+  const float* table;  // codebook or HYB LUT (global)
+  float* trace;        // (B, N, 2^L) cumulative costs
+  int32_t* backptr;    // (B, N, 2^L) chosen predecessor states
+  long long B;
+  int N, L, Q;
+};
+
 // Bitstream layouts (the values of BCJR_BITS_* in the C ABI).
 enum { BITS_FMT_U8 = 0, BITS_FMT_I32 = 1, BITS_FMT_PACKED = 2 };
 

@@ -38,6 +38,7 @@ const void* fwd4_kernel_ptr(int code, int upt);
 const void* bwd_kernel_ptr(int KV, int V, int code, int upt);
 const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache, bool wide);
 const void* decode_kernel_ptr(int KV, int V, int code);
+const void* trace_kernel_ptr(int KV, int V, int code);
 const void* dequant_kernel_ptr(int KV, int V, int code, bool vec4);
 const void* dequant_t16_kernel_ptr(int KV, int V, int code, int fmt);
 const void* codebook_kernel_ptr(int code);

@@ -405,6 +405,86 @@ __global__ __launch_bounds__(256) void bcjr_decode_kernel(DecParams P) {
   }
 }
 
+// The full lattice of the min-sum recursion, for viterbi_encode_v(...,
+// return_trace=True) (src/viterbi/encode.py:250-307): trace[t][s] = cum_t(s)
+// and backptr[t][s] = the predecessor state the minimum chose, for every state s
+// of every step, with the rounding and tie rules of the Viterbi kernel above.
+// A diagnostic of one or a few sequences: one workgroup per sequence
+// (grid-stride), the reduced vector m_{t-1}(j) = min_p cum_{t-1}(p*NT + j) and
+// its argmin p in LDS (NT floats + NT bytes).  Thread tid owns the reduced
+// indices j = tid + i*nthr and, for each, the R states p*NT + j, whose
+// predecessors are the states p'*NT + (s >> kV):
+//   cum_t(s) = fl(m_{t-1}(s >> kV) + E_t(s)),
+//   backptr_t(s) = argmin_{t-1}(s >> kV) * NT + (s >> kV),
+// and m_t(j), argmin_t(j) over its R states (lowest p on a tie) are written
+// back after a barrier.  cum_{-1} = 0: m = 0 and argmin = 0 at the start.
+template <int KV, int V, int CODE>
+__global__ __launch_bounds__(1024) void bcjr_viterbi_trace_kernel(TraceParams P) {
+  constexpr int R = 1 << KV;
+  constexpr int kMaxJ = 16;  // reduced indices per thread: NT <= 16 * 1024
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int L = P.L, N = P.N;
+  const int NT = 1 << (L - KV);
+  const size_t S = (size_t)1 << L;
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  float* mprev = reinterpret_cast<float*>(smem);                // NT
+  uint8_t* aprev = reinterpret_cast<uint8_t*>(mprev + NT);       // NT
+  for (long long b = blockIdx.x; b < P.B; b += gridDim.x) {
+    for (int j = tid; j < NT; j += nthr) {
+      mprev[j] = 0.0f;
+      aprev[j] = 0;
+    }
+    __syncthreads();
+    for (int t = 0; t < N; ++t) {
+      float w[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) w[v] = P.seq[((size_t)b * N + t) * V + v];
+      float* tr = P.trace + ((size_t)b * N + t) * S;
+      int32_t* bp = P.backptr + ((size_t)b * N + t) * S;
+      float mnew[kMaxJ];
+      int anew[kMaxJ];
+#pragma unroll
+      for (int i = 0; i < kMaxJ; ++i) {
+        const int j = tid + i * nthr;
+        mnew[i] = 0.0f;
+        anew[i] = 0;
+        if (j < NT) {
+#pragma unroll 1
+          for (int p = 0; p < R; ++p) {
+            const uint32_t s = (uint32_t)p * (uint32_t)NT + (uint32_t)j;
+            float c[V];
+            codeword<CODE, V>(s, P.table, P.table, P.Q, c);
+            float e = 0.0f;
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              const float d = c[v] - w[v];
+              e = v ? e + d * d : d * d;
+            }
+            const uint32_t u = s >> KV;
+            const float cum = mprev[u] + e;
+            tr[s] = cum;
+            bp[s] = (int32_t)((uint32_t)aprev[u] * (uint32_t)NT + u);
+            if (p == 0 || cum < mnew[i]) {
+              mnew[i] = cum;
+              anew[i] = p;
+            }
+          }
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kMaxJ; ++i) {
+        const int j = tid + i * nthr;
+        if (j < NT) {
+          mprev[j] = mnew[i];
+          aprev[j] = (uint8_t)anew[i];
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
 // Dequantize tiles straight into the matrix: out[row, col] = fl32(scale * c_v(s_t))
 // (product in double, one rounding: the float64 product then float32 cast of
 // src/quantize/serialize.py:106 and src/rht/transform.py:110)
@@ -781,6 +861,24 @@ const void* decode_kernel_ptr(int KV, int V, int code) {
   BCJR_DEC_CASE(4, 1, CODE_3INST)
   BCJR_DEC_CASE(4, 2, CODE_TABLE)
   BCJR_DEC_CASE(4, 2, CODE_HYB)
+  return nullptr;
+}
+
+#define BCJR_TRACE_CASE(KV_, V_, CODE_) \
+  if (KV == KV_ && V == V_ && code == CODE_) return reinterpret_cast<const void*>(&bcjr_viterbi_trace_kernel<KV_, V_, CODE_>);
+
+const void* trace_kernel_ptr(int KV, int V, int code) {
+  BCJR_TRACE_CASE(1, 1, CODE_TABLE)
+  BCJR_TRACE_CASE(2, 1, CODE_TABLE)
+  BCJR_TRACE_CASE(2, 1, CODE_1MAD)
+  BCJR_TRACE_CASE(2, 1, CODE_3INST)
+  BCJR_TRACE_CASE(2, 2, CODE_TABLE)
+  BCJR_TRACE_CASE(2, 2, CODE_HYB)
+  BCJR_TRACE_CASE(4, 1, CODE_TABLE)
+  BCJR_TRACE_CASE(4, 1, CODE_1MAD)
+  BCJR_TRACE_CASE(4, 1, CODE_3INST)
+  BCJR_TRACE_CASE(4, 2, CODE_TABLE)
+  BCJR_TRACE_CASE(4, 2, CODE_HYB)
   return nullptr;
 }
 

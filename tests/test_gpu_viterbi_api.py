@@ -5,7 +5,9 @@ Bit-exact against the oracle (walk, bitstream, start, recon; mse to 1e-6): the
 constrained encoder of encode.py:328-389 (pinned on the CPU by brute force over
 the paths meeting the constraint), Algorithm 4 tail-biting (encode.py:392-422)
 and the reference's own tail-biting gates at L=16 (test_viterbi.py:135-197,
-test_viterbi_v2.py:98-147)."""
+test_viterbi_v2.py:98-147); the return_trace=True lattices (bcjr_viterbi_trace)
+bit-exact against the oracle's restatement of encode.py:250-307, including the
+reference's own trace gate shape (test_viterbi_cuda_forward.py:25-80)."""
 import numpy as np
 import pytest
 import torch
@@ -145,8 +147,6 @@ def test_numpy_api_matches_oracle(bcjr_mod, oracle):
     assert bs.dtype == np.int32 and np.array_equal(bs, b_r[0]) and st == int(s_r[0])
     assert np.array_equal(rc, r_r[0, :, 0]) and mse == float(np.mean((rc - seq) ** 2))
     assert np.array_equal(E.viterbi_decode(bs, st, L, k, dec1), rc)
-    with pytest.raises(NotImplementedError):
-        E.viterbi_encode(seq, L, k, dec1, return_trace=True)
 
     cb2 = rng.standard_normal((1 << L, 2)).astype(np.float32)
     dec2 = lambda s: cb2[s.astype(np.int64)]  # noqa: E731
@@ -175,3 +175,68 @@ def test_numpy_api_matches_oracle(bcjr_mod, oracle):
     # one step with a value whose two windows disagree: no walk, as the reference raises
     with pytest.raises(RuntimeError, match="No valid tail-biting walk"):
         E.viterbi_encode_constrained(seq[:1], L, k, dec1, L - k, 1)
+
+
+# (L, k, V, N, B, codebook) straight through ops.viterbi_trace
+TRACE = [
+    (6, 1, 1, 9, 3, "table"),     # kV = 1
+    (10, 2, 1, 40, 3, "1mad"),
+    (12, 2, 2, 24, 2, "hyb"),     # kV = 4
+    (8, 4, 1, 7, 2, "table"),     # kV = 4, V = 1
+    (16, 2, 1, 6, 2, "3inst"),    # 16 reduced indices per thread
+]
+
+
+@pytest.mark.parametrize("L,k,V,N,B,kind", TRACE)
+def test_viterbi_trace_bit_exact(bcjr_mod, oracle, L, k, V, N, B, kind):
+    _say(f"viterbi trace L={L} k={k} V={V} N={N} B={B} {kind}")
+    from bcjr import ops
+    rng = np.random.default_rng(L + 7 * N)
+    if kind == "hyb":
+        cb, cb_np = _codebook(bcjr_mod, kind, L, rng)
+    else:
+        cb_np = (oracle.codebook({"1mad": oracle.CODE_1MAD, "3inst": oracle.CODE_3INST}[kind], L) if kind != "table"
+                 else rng.standard_normal((1 << L, V)).astype(np.float32))
+        cb = torch.tensor(cb_np, device="cuda")
+    seq = rng.standard_normal((B, N, V)).astype(np.float32)
+    trace, bp = ops.viterbi_trace(ops.Spec(L, k, V, ops.CODE_TABLE), torch.tensor(seq, device="cuda"), cb)
+    trace, bp = trace.cpu().numpy(), bp.cpu().numpy()
+    for b in range(B):
+        t_r, b_r = oracle.viterbi_trace(seq[b], cb_np, L, k * V)
+        assert np.array_equal(trace[b], t_r), b
+        assert np.array_equal(bp[b], b_r), b
+
+
+def test_return_trace_api_and_reference_gate_shape(bcjr_mod, oracle):
+    """viterbi_encode / viterbi_encode_v with return_trace=True: the four usual
+    outputs unchanged, plus trace_err and backpointers bit-exact against the
+    oracle; at the reference's trace gate shape (L=16, k=2, V=2, HYB decoder,
+    256 weights) the final row is the cum_err that gate compares."""
+    _say("return_trace API")
+    from bcjr import encode as E
+    rng = np.random.default_rng(23)
+    L, k = 12, 2
+    cb1 = oracle.codebook(oracle.CODE_1MAD, L)[:, 0]
+    dec1 = lambda s: cb1[s.astype(np.int64)]  # noqa: E731
+    seq = rng.standard_normal(64).astype(np.float32)
+    out = E.viterbi_encode(seq, L, k, dec1, return_trace=True)
+    plain = E.viterbi_encode(seq, L, k, dec1)
+    assert len(out) == 6 and np.array_equal(out[0], plain[0]) and out[1] == plain[1]
+    assert np.array_equal(out[2], plain[2]) and out[3] == plain[3]
+    t_r, b_r = oracle.viterbi_trace(seq[:, None], cb1[:, None], L, k)
+    assert out[4].shape == (64, 1 << L) and out[4].dtype == np.float32 and out[5].dtype == np.int32
+    assert np.array_equal(out[4], t_r) and np.array_equal(out[5], b_r)
+    # backtrace through the returned backpointers gives the returned walk
+    w = [int(np.argmin(out[4][-1]))]
+    for t in range(63, 0, -1):
+        w.append(int(out[5][t, w[-1]]))
+    assert (np.array(w[::-1]) & 3).tolist() == out[0].tolist() and int(out[5][0, w[-1]]) == out[1]
+
+    lut = np.random.default_rng(2).standard_normal((512, 2)).astype(np.float32)
+    cbh = bcjr_mod.make_hyb_codebook_gpu(lut, Q=9, L_bits=16, device="cuda").cpu().numpy()
+    dech = lambda s: cbh[s.astype(np.int64)]  # noqa: E731
+    seq2 = rng.standard_normal(256).astype(np.float32)
+    out = E.viterbi_encode_v(seq2, 16, 2, 2, dech, return_trace=True)
+    t_r, b_r = oracle.viterbi_trace(seq2.reshape(128, 2), cbh, 16, 4)
+    assert np.array_equal(out[4], t_r) and np.array_equal(out[5], b_r)
+    assert int(np.argmin(out[4][-1])) == int(np.argmin(t_r[-1]))

@@ -195,6 +195,45 @@ def test_viterbi_is_min_cost_path(oracle, L, KV, V, N):
         assert (w2 == walk).all() and (r2 == recon).all()
 
 
+@pytest.mark.parametrize("L,KV,V,N", [(4, 2, 1, 5), (4, 2, 2, 4), (5, 1, 1, 6), (8, 4, 2, 3)])
+def test_viterbi_trace_vs_brute_force(oracle, L, KV, V, N):
+    """cum_t(s) is the smallest float32 prefix cost over the paths through s at
+    step t (fl(x + E) is monotone in x, so the recursion's minimum equals it
+    bit for bit) and the backpointer is the lowest predecessor attaining the
+    previous step's minimum; the backtrace from the final argmin is the C
+    encoder's walk, with its start state."""
+    rng = np.random.default_rng(10 * L + N)
+    paths = oracle.enumerate_paths(L, KV, N)
+    S, R = 1 << L, 1 << KV
+    for rep in range(6):
+        cb = rng.standard_normal((S, V)).astype(np.float32)
+        if rep == 5:
+            cb = np.round(cb * 2) / 2  # coarse codewords: ties between predecessors
+        seq = rng.standard_normal((1, N, V)).astype(np.float32)
+        trace, bp = oracle.viterbi_trace(seq[0], cb, L, KV)
+        prefix = np.zeros(len(paths), np.float32)
+        best = np.zeros((N, S), np.float32)
+        for t in range(N):
+            prefix = (prefix + _f32_path_costs(paths[:, t:t + 1], cb, seq[0, t:t + 1])).astype(np.float32)
+            b = np.full(S, np.inf, np.float32)
+            np.minimum.at(b, paths[:, t], prefix)
+            best[t] = b
+        assert np.array_equal(trace, best)
+        s = np.arange(S)
+        assert np.array_equal(bp[0], s >> KV)
+        for t in range(1, N):
+            preds = (np.arange(R)[None, :] << (L - KV)) | (s[:, None] >> KV)
+            costs = best[t - 1][preds]
+            want = preds[s, np.argmax(costs == costs.min(axis=1, keepdims=True), axis=1)]
+            assert np.array_equal(bp[t], want)
+        walk, _, start, _, _ = oracle.viterbi(seq, cb, L, KV)
+        w = np.empty(N, np.int64)
+        w[-1] = int(np.argmin(trace[-1]))
+        for t in range(N - 1, 0, -1):
+            w[t - 1] = bp[t, w[t]]
+        assert w.tolist() == walk[0].tolist() and int(bp[0, w[0]]) == int(start[0])
+
+
 def test_viterbi_tie_rules(oracle):
     """All-equal codewords: every path ties.  Lowest p at every step and lowest
     final state give the all-zero walk (encode.py:283-296)."""
