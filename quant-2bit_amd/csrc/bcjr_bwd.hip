@@ -41,7 +41,7 @@ namespace bcjr {
 template <int R>
 constexpr int kOuterUnroll = R <= 4 ? R : 1;
 
-template <int KV, int V, int CODE, int UPT, int CU>
+template <int KV, int V, int CODE, int UPT, int CU, int CUA>
 __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_COL ? 3 : 1) void bcjr_bwd_kernel(BwdParams P) {
   constexpr int R = 1 << KV;
   // Butterflies whose slot inputs are in flight ahead of the beta sweep's use
@@ -53,8 +53,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   // read those inputs from the slot as they go (the loop unrolled on the HYB
   // column walk, whose LUT offsets are then immediates).
   constexpr bool kPair = R <= 4;
-  static_assert(CU == 0 || kPair, "codeword cache is for butterflies of at most 4 states");
-  static_assert(CU <= UPT, "at most UPT cached butterflies");
+  static_assert((CU == 0 && CUA == 0) || kPair, "codeword cache is for butterflies of at most 4 states");
+  static_assert(CU <= UPT && CUA <= UPT, "at most UPT cached butterflies");
   constexpr bool kCol = CODE == CODE_HYB_COL;  // HYB column walk: one butterfly per thread
   static_assert(!kCol || (KV == 4 && UPT == 1), "the column walk is for L = 16, kV = 4");
   constexpr bool kColUnroll = kCol;  // outputs unrolled: immediate LUT offsets
@@ -100,23 +100,26 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
     for (int c = 0; c < R; ++c) cbs[c] = hyb_col_base((uint32_t)(R * min(tid, NB - 1) + c), P.Q);
   }
 
-  // Raw codewords h of this thread's first CU butterflies (hc[i][p][c] for
-  // state p*NT + R*u + c), fixed for the whole launch; the others are hashed
-  // per state in each sweep.
-  float hc[CU > 0 ? CU : 1][CU > 0 ? R : 1][CU > 0 ? R : 1][V];
-  if constexpr (CU > 0) {
+  // Raw codewords h of this thread's first NC butterflies (hcx[i][p][c] for
+  // state p*NT + R*u + c); the others are hashed per state.  Each sweep fills
+  // its own cache when it starts (CUA butterflies for alpha + mu, CU for beta
+  // + nu + grad, whose working set is larger), so neither cache is live in the
+  // other sweep.  The opaque thread index keeps the fill inside the sequence
+  // loop instead of hoisted to the launch, where both caches would be live.
+  auto fill_cache = [&](auto& hcx, auto count_tag) {
+    constexpr int NC = decltype(count_tag)::value;
 #pragma unroll
-    for (int i = 0; i < CU; ++i) {
-      const int u = min(tid + i * nthr, NB - 1);
+    for (int i = 0; i < NC; ++i) {
+      const int u = min(opaque(tid) + i * nthr, NB - 1);
       const uint32_t xu = CT::A * (uint32_t)(R * u) + CT::B;
 #pragma unroll
       for (int p = 0; p < R; ++p)
 #pragma unroll
         for (int c = 0; c < R; ++c)
           raw_codeword<CODE, V>(xu, CT::A * (uint32_t)(p * NT + c), (uint32_t)(p * NT + R * u + c), P.table, lut,
-                                P.Q, hc[i][p][c]);
+                                P.Q, hcx[i][p][c]);
     }
-  }
+  };
 
   // Byte address of slot k of butterfly tid + i*nthr at rotation rho:
   // 8 S(rotr(tid + i*nthr + k*NB)) = yb ^ unit_off(i) ^ slot_off(k), the last
@@ -186,6 +189,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
       using Fast = std::integral_constant<bool, EXACT>;
 
       // --------------------------- alpha + mu sweep ----------------------------
+      float hca[CUA > 0 ? CUA : 1][CUA > 0 ? R : 1][CUA > 0 ? R : 1][V];
+      fill_cache(hca, std::integral_constant<int, CUA>{});
       double C = 0.0;  // C_{t-1}
       int k = 0;
       int rho = nb - KV;  // kV * (t - 1) mod nb at t = 0
@@ -229,9 +234,9 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
           for (int p = 0; p < R; ++p) {
             float h[V];
-            if (i < CU) {
+            if (i < CUA) {
 #pragma unroll
-              for (int v = 0; v < V; ++v) h[v] = hc[i < CU ? i : 0][p][r][v];
+              for (int v = 0; v < V; ++v) h[v] = hca[i < CUA ? i : 0][p][r][v];
             } else if constexpr (kCol) {
               const float2 cw = hyb_col_read(lutb, cb + hyb_col_step(p, r));
               h[0] = cw.x;
@@ -295,7 +300,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           }
           if (i + 1 < UPT) read_in(i + 1, nx, nxu);
           if (q < NB) {
-            const int u = i < CU ? q : opaque(q);
+            const int u = i < CUA ? q : opaque(q);
             {
               float* dst = slot + ((size_t)t * NB + u) * 2 * R;
               store_vec<R>(dst, mi);
@@ -404,6 +409,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
       __syncthreads();
 
       // -------------------------- beta + nu + grad sweep -----------------------
+      float hcb[CU > 0 ? CU : 1][CU > 0 ? R : 1][CU > 0 ? R : 1][V];
+      fill_cache(hcb, std::integral_constant<int, CU>{});
       // Raw alpha-side inputs (m~, mu) of step t come back from HBM two
       // butterflies ahead of their use, across step boundaries.
       auto slot_src = [&](int t, int i) {
@@ -471,7 +478,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           for (int c = 0; c < R; ++c) {
             if (i < CU) {
 #pragma unroll
-              for (int v = 0; v < V; ++v) hh[c][v] = hc[i < CU ? i : 0][p][c][v];
+              for (int v = 0; v < V; ++v) hh[c][v] = hcb[i < CU ? i : 0][p][c][v];
             } else if constexpr (kCol) {
               const float2 cw = hyb_col_read(lutb, cbs[c] + hyb_col_step(p, c));
               hh[c][0] = cw.x;
@@ -699,7 +706,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #define BCJR_BWD_CASE(KV_, V_, CODE_, UPT_)                                                  \
   if (KV == KV_ && V == V_ && code == CODE_ && upt == UPT_)                                 \
     return reinterpret_cast<const void*>(                                                   \
-        &bcjr_bwd_kernel<KV_, V_, CODE_, UPT_, bwd_cached_units(KV_, V_, UPT_)>);
+        &bcjr_bwd_kernel<KV_, V_, CODE_, UPT_, bwd_cached_units(KV_, V_, UPT_),          \
+                         bwd_alpha_cached_units(KV_, V_, UPT_)>);
 
 #define BCJR_BWD_UPTS(KV_, V_, CODE_) \
   BCJR_BWD_CASE(KV_, V_, CODE_, 1)    \

@@ -31,6 +31,16 @@ constexpr int bwd_cached_units(int KV, int V, int upt) {
                                                                         : kBwdCacheVgprs / ((1 << KV) * (1 << KV) * V));
 }
 
+// The alpha + mu sweep's own budget (its working set is smaller than the beta
+// + nu + grad sweep's, and the two caches are never live together).
+constexpr int kBwdAlphaCacheVgprs = 128;
+constexpr int bwd_alpha_cached_units(int KV, int V, int upt) {
+  return KV >= 4 ? 0
+                 : (upt < kBwdAlphaCacheVgprs / ((1 << KV) * (1 << KV) * V)
+                        ? upt
+                        : kBwdAlphaCacheVgprs / ((1 << KV) * (1 << KV) * V));
+}
+
 const void* fwd_kernel_ptr(int KV, int V, int code, int upt, bool internals);
 // The four-waves-per-SIMD forward (bcjr_fwd4.hip): kV = 2, V = 1, codes TABLE /
 // 1MAD / 3INST, 1024 threads, upt = 2^(L-14) butterflies per thread (L = 14..16).
