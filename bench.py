@@ -74,7 +74,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="layer", choices=["layer", "tile", "cpu"])
+    ap.add_argument("--config", default="layer", choices=["layer", "tile", "qat", "dequant", "cpu"],
+                    help="layer: the headline line; tile / qat / dequant: one secondary leg alone (for profiling); "
+                         "cpu: the CPU-runnable config on the GPU")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layer-tiles", type=int, default=7,
                     help="layer tiles in the torch CPU baseline sample (L=16; ~5-15 s each)")
@@ -398,6 +400,11 @@ def dequant_layer(torch, bcjr, ops, dev):
         W = ops.dequant(spec, start, cb._bcjr_lut, rows, cols, 16, 16, 0.02, packed=packed)
         bcjr.apply_inverse_rht_gpu(W, sl, sr)
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        # A few ms of spin ahead of the events, so the host has enqueued both
+        # launches before the first event fires: the events then bracket the
+        # kernels alone, not the host's enqueue gap (longer than a 4 M-weight
+        # dequant).
+        torch.cuda._sleep(5_000_000)
         e[0].record(stream)
         W = ops.dequant(spec, start, cb._bcjr_lut, rows, cols, 16, 16, 0.02, packed=packed)
         e[1].record(stream)
@@ -508,11 +515,6 @@ def main():
               flush=True)
         return
 
-    layer = Layer(torch, bcjr, dev)
-    layer.spec, _ = bcjr.codes.resolve_codebook(layer.cb, 16, 2, 1, dev)
-    cells = float(LAYER_SEQS) * 256 * 65536
-    stream = torch.cuda.current_stream(dev)
-
     if args.config == "tile":
         res = tile_config(torch, bcjr, ops, dev, exp_peak)
         calibration_copy(torch, dev)
@@ -522,6 +524,18 @@ def main():
                           "data": "synthetic N(0,1)", "config": {"workload": res["workload"]}, "tile": res}),
               flush=True)
         return
+
+    if args.config in ("qat", "dequant"):  # one secondary leg alone, for the profiler
+        res = (qat_shape(torch, bcjr, ops, dev, exp_peak) if args.config == "qat"
+               else dequant_layer(torch, bcjr, ops, dev))
+        calibration_copy(torch, dev)
+        print(json.dumps({"config": args.config, args.config: res}), flush=True)
+        return
+
+    layer = Layer(torch, bcjr, dev)
+    layer.spec, _ = bcjr.codes.resolve_codebook(layer.cb, 16, 2, 1, dev)
+    cells = float(LAYER_SEQS) * 256 * 65536
+    stream = torch.cuda.current_stream(dev)
 
     # ---- the layer QAT step, timed whole ----
     ms_step = None
