@@ -106,6 +106,9 @@ CASES = [
     (16, 2, 2, 64, 2, "hyb", 0.1),       # reference QAT trellis (L=16, kV=4)
     (16, 2, 1, 1024, 1, "3inst", 0.1),   # long sequence: per-step partials are double-buffered
     (16, 2, 1, 128, 2, "table", 0.2),    # table codebook on the 1024-thread forward
+    (16, 2, 1, 64, 2, "1mad", 0.2),      # 1MAD group-sum variant: every alpha + mu butterfly cached
+    (16, 1, 2, 64, 2, "hyb", 0.3),       # k = 1, V = 2 at L = 16: 8 two-dimensional butterflies per thread
+    (16, 1, 2, 64, 2, "table", 0.15),
     (14, 2, 1, 64, 3, "1mad", 0.05),     # 1024-thread forward, exact variant, 1 butterfly per thread
     (15, 2, 1, 64, 2, "3inst", 0.07),    # 1024-thread forward, exact variant, 2 per thread
     (15, 2, 1, 64, 2, "table", 0.3),
