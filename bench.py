@@ -290,9 +290,17 @@ def tile_config(torch, bcjr, ops, dev, exp_peak, B=4096, T=0.1):
     torch.cuda.synchronize(dev)
     f = e[0].elapsed_time(e[1]) / 1e3 / reps
     b = e[1].elapsed_time(e[2]) / 1e3 / reps
+    # the forward's diagnostics variant with the fused marginal entropy (entropy_diagnostic)
+    ops.forward_entropy(spec, x, T, None)
+    e[0].record(stream)
+    ops.forward_entropy(spec, x, T, None)
+    e[1].record(stream)
+    torch.cuda.synchronize(dev)
+    fe = e[0].elapsed_time(e[1]) / 1e3
     cells = float(B) * 256 * 65536
     return {"workload": "single-tile: L=16 k=2 V=1 N=256 B=4096 (1024x1024 matrix), 3INST, T=0.1",
-            "fwd_ms": f * 1e3, "bwd_ms": b * 1e3, "state_updates_per_s": 4.0 * cells / (f + b),
+            "fwd_ms": f * 1e3, "bwd_ms": b * 1e3, "fwd_entropy_ms": fe * 1e3,
+            "state_updates_per_s": 4.0 * cells / (f + b),
             "roofline_frac": trans_per_cell_grad(2) * cells / (f + b) / exp_peak}
 
 
