@@ -269,6 +269,22 @@ def test_undersized_workspace_is_reported_before_any_device_call(lib, op):
     assert f"({slot} bytes)" in msg and "100 bytes" in msg
 
 
+def test_viterbi_trace_validates_before_any_device_call(lib):
+    """bcjr_viterbi_trace refuses bad problems and missing pointers on the host
+    (no device needed), and an empty batch is a no-op."""
+    import bcjr._lib as BL
+    d = ctypes.c_void_p(4096)
+    p = BL.Problem(16, 2, 1, 2, 64, 0, 9, 0)
+    assert lib.bcjr_viterbi_trace(ctypes.byref(p), d, d, None, d, None) == BL.BCJR_EINVAL
+    assert "non-NULL" in lib.bcjr_last_error().decode()
+    assert lib.bcjr_viterbi_trace(ctypes.byref(p), d, None, d, d, None) == BL.BCJR_EINVAL
+    assert "codebook" in lib.bcjr_last_error().decode()
+    p = BL.Problem(17, 2, 1, 2, 64, 0, 9, 0)
+    assert lib.bcjr_viterbi_trace(ctypes.byref(p), d, d, d, d, None) == BL.BCJR_EUNSUPPORTED
+    p = BL.Problem(16, 2, 1, 0, 64, 2, 9, 0)
+    assert lib.bcjr_viterbi_trace(ctypes.byref(p), None, None, None, None, None) == BL.BCJR_OK
+
+
 def test_workspace_check_passes_for_empty_batch(lib):
     import bcjr._lib as BL
     p = BL.Problem(16, 2, 1, 0, 256, 2, 9, 0)
