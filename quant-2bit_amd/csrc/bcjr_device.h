@@ -259,6 +259,12 @@ __device__ __forceinline__ void raw_codeword(uint32_t xu, uint32_t off, uint32_t
 // waves, so sequences with a lower temperature use the group maxima throughout.
 constexpr float kUnderflow = 0x1p-120f;
 constexpr float kExactBelowT = 0.08f;
+// The 1024-thread forward's switch point.  Its exact variant hashes every
+// codeword (the cache does not fit beside that variant's working set in 128
+// VGPRs), so its group-sum variant, recomputes included, stays the faster one
+// down to T = 0.045 on Gaussian weights at L = 16 (at 0.05: 45 against 51 ms
+// per 4,096 sequences; at 0.04 they are even).
+constexpr float kExactBelowTFwd4 = 0.045f;
 
 // Load / store n consecutive floats (16-byte aligned when n % 4 == 0, 8-byte
 // aligned when n == 2).

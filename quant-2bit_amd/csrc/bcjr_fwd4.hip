@@ -122,7 +122,7 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
       // The group-sum variant keeps the thread's 16*UPT codewords in VGPRs for the
       // sequence (formed here, per sequence: the opaque thread index keeps them
       // from being hoisted into a launch-long live range).  The exact-maximum
-      // variant (T < kExactBelowT) forms each codeword where it is used, which
+      // variant (T < kExactBelowTFwd4) forms each codeword where it is used, which
       // leaves its larger working set the registers the cache would hold.
       float hc[EXACT ? 1 : UPT][EXACT ? 1 : R][EXACT ? 1 : R];
       if constexpr (!EXACT) {
@@ -383,7 +383,7 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
       }
       return logZ2;
     };
-    const double logZ2 = Tb < kExactBelowT ? sweeps(std::true_type{}) : sweeps(std::false_type{});
+    const double logZ2 = Tb < kExactBelowTFwd4 ? sweeps(std::true_type{}) : sweeps(std::false_type{});
 
     // soft of step 0: the last beta step (k = 2N - 1, odd) wrote buffer 1
     if (tid == 0) {

@@ -113,14 +113,15 @@ def _max_blocks(bcjr_mod, op, B):
 
 def test_layer_kernel_instance_slot_reuse_and_mixed_T(bcjr_mod, oracle, cb3):
     """The layer's kernel instance with every workgroup running 4 sequences in a
-    row on its slot, T switching between the exact (< 0.08) and group-sum
-    variants from one sequence to the next."""
+    row on its slot, T switching between the exact and group-sum variants from
+    one sequence to the next (the backward switches at 0.08, the 1024-thread
+    forward at 0.045)."""
     from bcjr import _lib, ops
     cb, cb_np = cb3
     G = min(_max_blocks(bcjr_mod, _lib.OP_FORWARD, 1 << 20), _max_blocks(bcjr_mod, _lib.OP_BACKWARD, 1 << 20))
     B = 4 * G + 16
     _say(f"layer instance: B={B} (resident workgroups {G})")
-    TS = np.array([0.05, 0.3, 0.07, 0.12, 0.5], dtype=np.float32)
+    TS = np.array([0.05, 0.3, 0.03, 0.12, 0.07, 0.5], dtype=np.float32)
     T_np = TS[(np.arange(B) // G) % len(TS)]
     seq = np.random.default_rng(0).standard_normal((B, N, V)).astype(np.float32)
     g = np.random.default_rng(1).standard_normal((B, N, V)).astype(np.float32)

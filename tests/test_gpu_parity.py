@@ -109,8 +109,12 @@ CASES = [
     (16, 2, 1, 64, 2, "1mad", 0.2),      # 1MAD group-sum variant: every alpha + mu butterfly cached
     (16, 1, 2, 64, 2, "hyb", 0.3),       # k = 1, V = 2 at L = 16: 8 two-dimensional butterflies per thread
     (16, 1, 2, 64, 2, "table", 0.15),
-    (14, 2, 1, 64, 3, "1mad", 0.05),     # 1024-thread forward, exact variant, 1 butterfly per thread
-    (15, 2, 1, 64, 2, "3inst", 0.07),    # 1024-thread forward, exact variant, 2 per thread
+    (14, 2, 1, 64, 3, "1mad", 0.05),     # 1024-thread forward, group-sum variant below 0.08, 1 butterfly per thread
+    (15, 2, 1, 64, 2, "3inst", 0.07),    # the same, 2 per thread
+    (14, 2, 1, 64, 3, "1mad", 0.03),     # 1024-thread forward, exact variant, 1 butterfly per thread
+    (15, 2, 1, 64, 2, "3inst", 0.04),    # 1024-thread forward, exact variant, 2 per thread
+    (16, 2, 1, 64, 2, "3inst", 0.045),   # the 1024-thread forward's switch point
+    (16, 2, 1, 64, 2, "3inst", 0.06),
     (15, 2, 1, 64, 2, "table", 0.3),
 ]
 
