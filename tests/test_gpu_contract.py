@@ -94,9 +94,10 @@ def test_untagged_codebooks_reach_the_generator_kernels(bcjr_mod, L, k, V, N, ki
         assert resolve_codebook(plain, L, k, V, dev)[0].code == ops.CODE_TABLE
 
 
-def test_non_finite_inputs_give_nan_for_their_sequences(bcjr_mod, oracle):
-    _say("non-finite inputs")
-    L, N, B = 12, 64, 8
+@pytest.mark.parametrize("L", [12, 14, 16])  # 512-thread forward; 1024-thread forward at 1 and 4 butterflies per thread
+def test_non_finite_inputs_give_nan_for_their_sequences(bcjr_mod, oracle, L):
+    _say(f"non-finite inputs L={L}")
+    N, B = 64, 8
     cb = bcjr_mod.make_1mad_codebook(L, "cuda")
     cb_np = cb.cpu().numpy()
     rng = np.random.default_rng(3)
