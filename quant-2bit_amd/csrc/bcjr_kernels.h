@@ -23,8 +23,10 @@ constexpr int fwd_cached_units(int KV, int V, int upt) {
                                                                         : kFwdCacheVgprs / ((1 << KV) * (1 << KV) * V));
 }
 
-// The same budget for the backward.
-constexpr int kBwdCacheVgprs = 64;
+// The same budget for the backward's beta + nu + grad sweep: 5 of 8
+// butterflies at kV = 2, V = 1 (80 VGPRs beside that sweep's working set;
+// a sixth fits but measured the same), 2 at V = 2.
+constexpr int kBwdCacheVgprs = 80;
 constexpr int bwd_cached_units(int KV, int V, int upt) {
   return KV >= 4 ? 0
                  : (upt < kBwdCacheVgprs / ((1 << KV) * (1 << KV) * V) ? upt
