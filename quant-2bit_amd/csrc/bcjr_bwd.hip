@@ -24,9 +24,10 @@
 // pairs, in the in-place rotated layout of Swizzle: a thread reads its
 // butterfly's R pairs, computes, and writes its R outputs to the same pairs, with
 // one barrier per step and the next butterfly's pairs read ahead of the current
-// one's arithmetic.  The alpha sweep writes each butterfly's raw inputs (m~ and
-// mu, 2R floats) to the scratch slot; the beta sweep reads them back two
-// butterflies ahead to form P and phi.  The codewords of a thread's first few
+// one's arithmetic.  The alpha sweep writes each butterfly's raw inputs to the
+// scratch slot as R (m~, mu) pairs, [m~_0 mu_0 m~_1 mu_1 ...], the form in which
+// they leave LDS; the beta sweep reads them back two butterflies ahead to form
+// P and phi.  The codewords of a thread's first few
 // butterflies stay in VGPRs for the launch (bwd_cached_units).
 //
 // Group sums take the zero-shift form; a butterfly with any
@@ -40,6 +41,28 @@ namespace bcjr {
 // Unroll of the loop over a butterfly's outputs: full for 2 or 4 states.
 template <int R>
 constexpr int kOuterUnroll = R <= 4 ? R : 1;
+
+// A butterfly's slot entry: R (m~, mu) pairs, 8-byte aligned.  Each pair is
+// stored from the two registers the LDS read filled, so no register moves
+// assemble a wider store.
+template <int R>
+__device__ __forceinline__ void store_pairs(float* dst, const float (&m)[R], const float (&mu)[R]) {
+#pragma unroll
+  for (int p = 0; p < R; ++p) *reinterpret_cast<float2*>(dst + 2 * p) = make_float2(m[p], mu[p]);
+}
+// ... read back 16 bytes (two pairs) at a time (16-byte aligned, R even).
+template <int R>
+__device__ __forceinline__ void load_pairs(const float* src, float (&m)[R], float (&mu)[R]) {
+  static_assert(R % 2 == 0, "pairs are read two at a time");
+#pragma unroll
+  for (int p = 0; p < R; p += 2) {
+    const float4 v = *reinterpret_cast<const float4*>(src + 2 * p);
+    m[p] = v.x;
+    mu[p] = v.y;
+    m[p + 1] = v.z;
+    mu[p + 1] = v.w;
+  }
+}
 
 template <int KV, int V, int CODE, int UPT, int CU, int CUA>
 __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_COL ? 3 : 1) void bcjr_bwd_kernel(BwdParams P) {
@@ -302,13 +325,9 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           if (q < NB) {
             const int u = i < CUA ? q : opaque(q);
             {
-              float* dst = slot + ((size_t)t * NB + u) * 2 * R;
-              store_vec<R>(dst, mi);
-              store_vec<R>(dst + R, mui);
+              store_pairs(slot + ((size_t)t * NB + u) * 2 * R, mi, mui);
             }
-            float Mu = mi[0];
-#pragma unroll
-            for (int p = 1; p < R; ++p) Mu = fmaxf(Mu, mi[p]);
+            const float Mu = max_of_inputs(mi);
             const float sh = -Mu;
             float m[R];
 #pragma unroll
@@ -426,8 +445,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         for (int d = 0; d < kSlotAhead; ++d) {
           const int tt = N - 1 - d / UPT;
           if (tt >= 0) {
-            load_vec<R>(slot_src(tt, d % UPT), pf[d]);
-            load_vec<R>(slot_src(tt, d % UPT) + R, pfu[d]);
+            load_pairs(slot_src(tt, d % UPT), pf[d], pfu[d]);
           }
         }
       }
@@ -564,16 +582,13 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
             const int tt = t - (i + kSlotAhead) / UPT;
             const int ii = (i + kSlotAhead) % UPT;
             if (tt >= 0) {
-              load_vec<R>(slot_src(tt, ii), pf[kSlotAhead - 1]);
-              load_vec<R>(slot_src(tt, ii) + R, pfu[kSlotAhead - 1]);
+              load_pairs(slot_src(tt, ii), pf[kSlotAhead - 1], pfu[kSlotAhead - 1]);
             }
           }
           if (i + 1 < UPT) read_in(i + 1, nx, nxu);
           if (q < NB) {
             const int u = i < CU ? q : opaque(q);
-            float Mu = ni[0];
-#pragma unroll
-            for (int c = 1; c < R; ++c) Mu = fmaxf(Mu, ni[c]);
+            const float Mu = max_of_inputs(ni);
             const float sh = -Mu;
             float nr[R];
 #pragma unroll
@@ -628,7 +643,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
               for (int p = 0; p < R; ++p) {
                 float no, nuo, a0, a1[V];
-                const float pms = src[p] + kts, pmup = src[R + p];
+                const float pms = src[2 * p] + kts, pmup = src[2 * p + 1];
                 const float s = beta_out(Fast{}, i, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
                 smin = p ? fminf(smin, s) : s;
                 ua0 += a0;
@@ -645,7 +660,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll 1
                   for (int p = 0; p < R; ++p) {
                     float no, nuo, a0, a1[V];
-                    const float pms = src[p] + kts, pmup = src[R + p];
+                    const float pms = src[2 * p] + kts, pmup = src[2 * p + 1];
                     beta_out(std::true_type{}, i, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
                     ua0 += a0;
 #pragma unroll
@@ -663,7 +678,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll kOuterUnroll<R>
               for (int p = 0; p < R; ++p) {
                 float no, nuo, a0, a1[V];
-                const float pms = src[p] + kts, pmup = src[R + p];
+                const float pms = src[2 * p] + kts, pmup = src[2 * p + 1];
                 const float s = beta_out(Fast{}, i, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
                 if (!EXACT && s < kUnderflow)
                   beta_out(std::true_type{}, i, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);

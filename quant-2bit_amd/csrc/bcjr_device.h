@@ -303,6 +303,37 @@ __device__ __forceinline__ void store_vec(float* dst, const float* src) {
   }
 }
 
+// Maximum of a butterfly's R inputs as read from LDS.  fmaxf on a loaded value
+// first quiets a possible signalling NaN (one v_max_f32 x, x per operand the
+// compiler cannot prove canonical); these values all come out of arithmetic, so
+// they never are one, and v_max3_f32 / v_max_f32 take them directly.  A quiet
+// NaN operand is skipped, as by fmaxf.
+__device__ __forceinline__ float vmax3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float vmax_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+template <int n>
+__device__ __forceinline__ float max_of_inputs(const float (&v)[n]) {
+  static_assert(n >= 2, "at least two inputs");
+  if constexpr (n == 2) {
+    return vmax_raw(v[0], v[1]);
+  } else if constexpr (n == 4) {
+    return vmax_raw(vmax3_raw(v[0], v[1], v[2]), v[3]);
+  } else {
+    float m = vmax3_raw(v[0], v[1], v[2]);
+#pragma unroll
+    for (int i = 3; i + 1 < n; i += 2) m = vmax3_raw(m, v[i], v[i + 1]);
+    if constexpr ((n - 3) % 2 == 1) m = vmax_raw(m, v[n - 1]);
+    return m;
+  }
+}
+
 // Returns x unchanged but opaque to the optimiser.  Kernels that recompute
 // codewords every step pass their butterfly index through this inside the step
 // loop; otherwise loop-invariant code motion hoists all R*R codewords per unit

@@ -268,9 +268,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
           if (q < NB) {
             const int u = i < CU ? q : opaque(q);
             store_vec<R>(slot + ((size_t)t * NB + u) * R, m);
-            float Mu = m[0];
-#pragma unroll
-            for (int p = 1; p < R; ++p) Mu = fmaxf(Mu, m[p]);
+            const float Mu = max_of_inputs(m);
             const float sh = -Mu;
 #pragma unroll
             for (int p = 0; p < R; ++p) m[p] += sh;
@@ -483,9 +481,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
           if (i + 1 < UPT) read_in(i + 1, nx);
           if (q < NB) {
             const int u = i < CU ? q : opaque(q);
-            float Mu = n[0];
-#pragma unroll
-            for (int c = 1; c < R; ++c) Mu = fmaxf(Mu, n[c]);
+            const float Mu = max_of_inputs(n);
             const float sh = -Mu;
             float nr[R];
 #pragma unroll

@@ -173,7 +173,7 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
             for (int p = 0; p < R; ++p) mx[p] = prev[p * NB + u + NTHR];
           }
           store_vec<R>(slot_t + R * u, m);
-          const float M = max4(m);
+          const float M = max_of_inputs(m);
 #pragma unroll
           for (int p = 0; p < R; ++p) m[p] -= M;
           const float off = M - O;
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
             if (tt >= 0) load_vec<R>(slot_src(tt, ii), pb);
           }
           if (i + 1 < UPT) load_vec<R>(prev + R * (u + NTHR), nx);
-          const float M = max4(n);
+          const float M = max_of_inputs(n);
 #pragma unroll
           for (int c = 0; c < R; ++c) n[c] -= M;
           const float kts = Kt + M;
