@@ -129,6 +129,11 @@ def _recognise(cb: torch.Tensor, L: int, V: int):
     return CODE_TABLE, 0, None
 
 
+# Bits per step (k*V) for which the generator codes (1MAD, 3INST, HYB) have
+# kernels of their own; at k*V = 1 only the table kernels are built.
+GENERATOR_KV = (2, 4)
+
+
 def _canonical(device) -> torch.device:
     """torch.device with the index filled in ('cuda' -> 'cuda:<current>')."""
     device = torch.device(device)
@@ -150,6 +155,12 @@ def resolve_codebook(codebook: torch.Tensor, L: int, k: int, V: int, device: tor
     device = _canonical(device)
     if _canonical(codebook.device) != device:
         raise AssertionError(f"codebook is on {codebook.device} but the sequences are on {device}")
+    if k * V not in GENERATOR_KV:
+        # No hashed or LUT kernels at this shape: any codebook is a table.
+        table = codebook.detach()
+        if table.dtype != torch.float32 or not table.is_contiguous():
+            table = table.to(torch.float32).contiguous()
+        return Spec(L, k, V, CODE_TABLE), table
     code = getattr(codebook, "_bcjr_code", None)
     if code is not None:
         if code == CODE_HYB:

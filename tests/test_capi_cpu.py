@@ -316,6 +316,19 @@ def test_tagged_hyb_lut_device_is_checked():
         resolve_codebook(cb, 8, 1, 2, torch.device("meta"))
 
 
+def test_one_bit_per_step_takes_the_table_kernels():
+    """k*V = 1 has table kernels only: a codebook tagged (or recognisable) as a
+    generator's output is handed to them as a table, not as a generator code
+    the library would refuse."""
+    from bcjr.codes import _tag, resolve_codebook
+    from bcjr._lib import CODE_3INST, CODE_TABLE
+    cb = _tag(torch.randn(1 << 6, 1), CODE_3INST)
+    spec, table = resolve_codebook(cb, 6, 1, 1, torch.device("cpu"))
+    assert spec.code == CODE_TABLE and table.data_ptr() == cb.data_ptr()
+    spec, table = resolve_codebook(cb, 6, 2, 1, torch.device("cpu"))
+    assert spec.code == CODE_3INST and table is None
+
+
 def test_registered_ops_have_fake_implementations():
     """bcjr::forward / bcjr::backward / bcjr::rht are torch operators whose
     fake (meta) implementations give the output shapes without a device."""
