@@ -90,3 +90,90 @@ def test_sweep_vs_oracle(bcjr_mod, oracle, L, k, V, N, B, kind, T, per_seq, tail
     assert np.array_equal(bits.cpu().numpy(), bits_r)
     assert np.array_equal(start.cpu().numpy(), start_r)
     assert np.array_equal(recon.cpu().numpy(), recon_r.reshape(B, N * V))
+
+
+def _rht_cases(n=40, seed=7):
+    """(E, m, n): the extremes of the supported range, then powers of two with
+    m*n <= 2^22, each batched E = 1..3 times."""
+    rng = np.random.default_rng(seed)
+    out = [(1, 1, 1), (1, 1, 16384), (2, 16384, 1), (1, 2, 8192), (1, 4096, 1024)]
+    while len(out) < n:
+        lm, ln = int(rng.integers(0, 15)), int(rng.integers(0, 15))
+        if lm + ln <= 22:
+            out.append((int(rng.integers(1, 4)), 1 << lm, 1 << ln))
+    return out
+
+
+@pytest.mark.parametrize("E,m,n", _rht_cases())
+def test_rht_sweep_vs_oracle(bcjr_mod, oracle, E, m, n):
+    """Forward and inverse RHT, batched and single, against the oracle's float32
+    butterflies: bit-exact when m*n is an even power of two (the scale 1/sqrt(mn)
+    is exact), within 2 ulp of the largest value otherwise."""
+    print(f"rht sweep E={E} {m}x{n}", flush=True)
+    rng = np.random.default_rng(E * 100003 + m * 31 + n)
+    W = _weights(rng, (E, m, n), tails=bool(m & 1))
+    SL = rng.choice([-1.0, 1.0], size=(E, m)).astype(np.float32)
+    SR = rng.choice([-1.0, 1.0], size=(E, n)).astype(np.float32)
+    Wd, sl, sr = (torch.tensor(a, device="cuda") for a in (W, SL, SR))
+    Wt = bcjr_mod.apply_rht_batched(Wd, sl, sr)
+    back = bcjr_mod.apply_inverse_rht_batched(Wt, sl, sr)
+    exact = ((m * n).bit_length() - 1) % 2 == 0
+    for e in range(E):
+        ref = oracle.rht(W[e], SL[e], SR[e])
+        ref_back = oracle.inverse_rht(Wt[e].cpu().numpy(), SL[e], SR[e])
+        got, got_back = Wt[e].cpu().numpy(), back[e].cpu().numpy()
+        if exact:
+            assert np.array_equal(got, ref)
+            assert np.array_equal(got_back, ref_back)
+        else:
+            assert np.abs(got - ref).max() <= 2 * np.spacing(np.abs(ref).max())
+            assert np.abs(got_back - ref_back).max() <= 2 * np.spacing(np.abs(ref_back).max())
+        assert torch.equal(Wt[e], bcjr_mod.apply_rht_gpu(Wd[e], sl[e], sr[e]))
+
+
+def _dequant_cases(n=32, seed=11):
+    """(L, k, V, kind, Tx, Ty, m, n): tiles of any shape holding whole steps,
+    matrices of 1..6 x 1..6 tiles."""
+    rng = np.random.default_rng(seed)
+    out = [(16, 2, 2, "hyb", 16, 16, 64, 256), (16, 2, 1, "3inst", 16, 16, 32, 64)]
+    while len(out) < n:
+        k, V = SHAPES[int(rng.integers(len(SHAPES)))]
+        kV = k * V
+        L = int(rng.integers(2 * kV, (11 if kV == 1 else 16) + 1))
+        kinds = ["table"] + (["1mad", "3inst"] if V == 1 else ["hyb"])
+        kind = kinds[int(rng.integers(len(kinds)))]
+        Tx, Ty = int(rng.choice([1, 2, 4, 8, 16, 3, 6])), int(rng.choice([1, 2, 4, 8, 16, 12, 5]))
+        if (Tx * Ty) % V:
+            continue
+        out.append((L, k, V, kind, Tx, Ty, Tx * int(rng.integers(1, 7)), Ty * int(rng.integers(1, 7))))
+    return out
+
+
+@pytest.mark.parametrize("L,k,V,kind,Tx,Ty,m,n", _dequant_cases())
+def test_dequant_sweep_vs_oracle(bcjr_mod, oracle, L, k, V, kind, Tx, Ty, m, n):
+    """The rotated-basis dequantization fl32(W_scale * c(walk)) from uint8 and
+    (where k*V divides 8) packed bitstreams, bit-exact against the oracle."""
+    from bcjr.serialize import dequant_target_gpu, pack_bitstreams
+    print(f"dequant sweep L={L} k={k} V={V} {kind} tiles {Tx}x{Ty} of {m}x{n}", flush=True)
+    rng = np.random.default_rng(L * 7919 + Tx * 131 + Ty * 17 + m + n)
+    cb, cb_np = _codebook(bcjr_mod, kind, L, V, rng)
+    kV = k * V
+    nc, nr, N = n // Ty, m // Tx, Tx * Ty // V
+    p = {
+        "bitstreams": rng.integers(0, 1 << kV, (nc, nr, N)).astype(np.uint8),
+        "start_states": rng.integers(0, 1 << L, (nc, nr)).astype(np.int32),
+        "sign_l": np.sign(rng.standard_normal(m)).astype(np.int8),
+        "sign_r": np.sign(rng.standard_normal(n)).astype(np.int8),
+        "W_scale": float(rng.uniform(0.005, 0.05)),
+        "shape": (m, n),
+        "config": {"L": L, "k": k, "V": V, "Tx": Tx, "Ty": Ty},
+    }
+    ref = (oracle.dequant_unit(p["bitstreams"], p["start_states"], cb_np, (m, n), L, kV, Tx, Ty)
+           * p["W_scale"]).astype(np.float32)
+    got = dequant_target_gpu(p, rotated=True, codebook=cb)
+    assert np.array_equal(got.cpu().numpy(), ref)
+    if 8 % kV == 0:
+        pk = {kk: v for kk, v in p.items() if kk != "bitstreams"}
+        pk["packed"] = pack_bitstreams(p["bitstreams"], kV)
+        pk["n_steps"] = N
+        assert torch.equal(dequant_target_gpu(pk, rotated=True, codebook=cb), got)
