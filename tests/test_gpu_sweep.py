@@ -177,3 +177,40 @@ def test_dequant_sweep_vs_oracle(bcjr_mod, oracle, L, k, V, kind, Tx, Ty, m, n):
         pk["packed"] = pack_bitstreams(p["bitstreams"], kV)
         pk["n_steps"] = N
         assert torch.equal(dequant_target_gpu(pk, rotated=True, codebook=cb), got)
+
+
+def _viterbi_cases(n=24, seed=13):
+    """(L, k, V, kind, N, B, overlap_bits): the constrained encoder over random
+    shapes, overlap windows from 0 bits (unconstrained) to L - kV (tail-biting)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        k, V = SHAPES[int(rng.integers(len(SHAPES)))]
+        kV = k * V
+        L = int(rng.integers(2 * kV, (11 if kV == 1 else 16) + 1))
+        kinds = ["table"] + (["1mad", "3inst"] if V == 1 else ["hyb"])
+        kind = kinds[int(rng.integers(len(kinds)))]
+        N = int(rng.choice(LENGTHS))
+        B = int(rng.integers(1, 9))
+        out.append((L, k, V, kind, N, B, int(rng.integers(0, L - kV + 1))))
+    return out
+
+
+@pytest.mark.parametrize("L,k,V,kind,N,B,ob", _viterbi_cases())
+def test_constrained_viterbi_sweep_vs_oracle(bcjr_mod, oracle, L, k, V, kind, N, B, ob):
+    """Walk, bitstream, start state (-1 where no walk meets the constraint) and
+    reconstruction bit-exact against the oracle's constrained encoder."""
+    print(f"constrained sweep L={L} k={k} V={V} {kind} N={N} B={B} ob={ob}", flush=True)
+    rng = np.random.default_rng(L * 613 + N * 7 + B + ob)
+    cb, cb_np = _codebook(bcjr_mod, kind, L, V, rng)
+    seq = _weights(rng, (B, N, V), tails=bool(N & 1))
+    ov = rng.integers(0, 1 << ob, B).astype(np.int32)
+    bits, start, recon, mse, out = bcjr_mod.viterbi_encode_constrained_v_batched_hip(
+        torch.tensor(seq.reshape(B, N * V), device="cuda"), cb, torch.tensor(ov, device="cuda"), ob,
+        L=L, k=k, V=V, return_all=True)
+    walk_r, bits_r, start_r, recon_r, _ = oracle.viterbi(seq, cb_np, L, k * V, overlap=ov, overlap_bits=ob)
+    assert np.array_equal(start.cpu().numpy(), start_r)
+    ok = start_r >= 0  # the other sequences' walks are unspecified
+    assert np.array_equal(out["walk"].cpu().numpy()[ok], walk_r[ok])
+    assert np.array_equal(bits.cpu().numpy()[ok], bits_r[ok])
+    assert np.array_equal(recon.cpu().numpy()[ok], recon_r.reshape(B, N * V)[ok])
