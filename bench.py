@@ -98,7 +98,7 @@ def measure_peaks(torch, dev):
                                      ctypes.c_int, ctypes.c_void_p]
     chains = lib.bcjr_peak_chains()
     n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
-    blocks = n_cu * 16  # 16 waves of 64 per CU (4 per SIMD)
+    blocks = n_cu * 16  # 16 blocks of 256 threads per CU: every SIMD as full as residency allows
     sink = torch.empty(blocks * 256, device=dev)
     stream = torch.cuda.current_stream(dev)
     out = {}
@@ -110,13 +110,16 @@ def measure_peaks(torch, dev):
     for name, kind, K in (("exp", 0, 0), ("log", 1, 0), ("fma", 2, 0), ("exp+2fma", 3, 2), ("exp+4fma", 3, 4)):
         iters = 4096
         run(kind, K, 64)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        run(kind, K, iters)
-        e1.record(stream)
-        torch.cuda.synchronize(dev)
-        sec = e0.elapsed_time(e1) / 1e3
-        out[name] = {"per_s": blocks * 256.0 * chains * iters / sec, "ms": sec * 1e3}
+        best = None
+        for _ in range(3):  # a peak: the fastest of three timed launches
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            run(kind, K, iters)
+            e1.record(stream)
+            torch.cuda.synchronize(dev)
+            sec = e0.elapsed_time(e1) / 1e3
+            best = sec if best is None else min(best, sec)
+        out[name] = {"per_s": blocks * 256.0 * chains * iters / best, "ms": best * 1e3}
     return out
 
 
