@@ -214,3 +214,80 @@ def test_constrained_viterbi_sweep_vs_oracle(bcjr_mod, oracle, L, k, V, kind, N,
     assert np.array_equal(out["walk"].cpu().numpy()[ok], walk_r[ok])
     assert np.array_equal(bits.cpu().numpy()[ok], bits_r[ok])
     assert np.array_equal(recon.cpu().numpy()[ok], recon_r.reshape(B, N * V)[ok])
+
+
+def _weight_cases(n=12, seed=17):
+    """(m, n, L, k, V, kind, T): one weight through bcjr_quantize_weight, shapes
+    of 1..32 16x16 tiles (powers of two for the RHT)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        m, nn = 1 << int(rng.integers(4, 10)), 1 << int(rng.integers(4, 10))
+        if m * nn > 8192:
+            continue
+        k, V = [(2, 1), (1, 2), (2, 2), (1, 1)][int(rng.integers(4))]
+        kV = k * V
+        L = int(rng.integers(max(2 * kV, 6), 13))
+        kinds = ["table"] + (["1mad", "3inst"] if V == 1 else ["hyb"])
+        kind = kinds[int(rng.integers(len(kinds)))]
+        T = round(float(np.exp(rng.uniform(np.log(0.05), np.log(1.0)))), 4)
+        out.append((m, nn, L, k, V, kind, T))
+    return out
+
+
+@pytest.mark.parametrize("m,n,L,k,V,kind,T", _weight_cases())
+def test_quantize_weight_sweep_vs_oracle(bcjr_mod, oracle, m, n, L, k, V, kind, T):
+    """bcjr_quantize_weight (RHT, RMS scale, 16x16 tiles, BCJR, back) and its
+    gradient against the same composition on the oracle."""
+    from bcjr.quant import tile_for_viterbi, untile_from_viterbi
+    print(f"quantize_weight sweep {m}x{n} L={L} k={k} V={V} {kind} T={T}", flush=True)
+    rng = np.random.default_rng(m * 131 + n * 7 + L)
+    cb, cb_np = _codebook(bcjr_mod, kind, L, V, rng)
+    W = (rng.standard_normal((m, n)) * 0.02).astype(np.float32)
+    g = rng.standard_normal((m, n)).astype(np.float32)
+    sl = rng.choice([-1.0, 1.0], size=m).astype(np.float32)
+    sr = rng.choice([-1.0, 1.0], size=n).astype(np.float32)
+    Wd = torch.tensor(W, device="cuda", requires_grad=True)
+    Wq = bcjr_mod.bcjr_quantize_weight(Wd, torch.tensor(sl, device="cuda"), torch.tensor(sr, device="cuda"),
+                                       cb, T, L=L, k=k, V=V)
+    (Wq * torch.tensor(g, device="cuda")).sum().backward()
+
+    Wt = oracle.rht(W, sl, sr)
+    scale = np.float32(np.sqrt((Wt ** 2).mean(dtype=np.float32)))
+    seqs, info = tile_for_viterbi(torch.tensor(Wt / scale), 16, 16)
+    seqs = seqs.numpy().reshape(seqs.shape[0], -1, V)
+    soft, _ = oracle.bcjr_forward(seqs, cb_np, T, L, k * V)
+    Wtq = untile_from_viterbi(torch.tensor(soft.reshape(seqs.shape[0], -1)), info, (m, n), 16, 16).numpy()
+    ref = oracle.inverse_rht(Wtq * scale, sl, sr)
+    assert np.abs(Wq.detach().cpu().numpy() - ref).max() <= SOFT_TOL * np.abs(ref).max()
+    gt_tiles, _ = tile_for_viterbi(torch.tensor(oracle.rht(g, sl, sr) * scale), 16, 16)
+    d_seq = oracle.bcjr_backward(seqs, cb_np, T, L, k * V, gt_tiles.numpy().reshape(seqs.shape))
+    d_wt = untile_from_viterbi(torch.tensor(d_seq.reshape(seqs.shape[0], -1) / scale), info, (m, n), 16, 16).numpy()
+    grad_ref = oracle.inverse_rht(d_wt, sl, sr)
+    assert np.abs(Wd.grad.cpu().numpy() - grad_ref).max() <= GRAD_TOL * np.abs(grad_ref).max()
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_experts_sweep_vs_per_weight_loop(bcjr_mod, seed):
+    """bcjr_quantize_experts over a random mixture of 2..7 weights of 1..4
+    distinct shapes (repeated shapes share one batched RHT), a temperature per
+    weight, against one bcjr_quantize_weight per weight: values and gradients."""
+    rng = np.random.default_rng(500 + seed)
+    palette = [(1 << int(rng.integers(4, 9)), 1 << int(rng.integers(4, 9))) for _ in range(int(rng.integers(1, 5)))]
+    shapes = [palette[int(rng.integers(len(palette)))] for _ in range(int(rng.integers(2, 8)))]
+    Ts = torch.tensor(np.exp(rng.uniform(np.log(0.05), np.log(0.5), len(shapes))).astype(np.float32), device="cuda")
+    print(f"experts sweep seed={seed} shapes={shapes}", flush=True)
+    cb = bcjr_mod.make_3inst_codebook(12, "cuda")
+    Ws = [torch.tensor((rng.standard_normal(s) * 0.02).astype(np.float32), device="cuda") for s in shapes]
+    sl = [torch.tensor(rng.choice([-1.0, 1.0], size=s[0]).astype(np.float32), device="cuda") for s in shapes]
+    sr = [torch.tensor(rng.choice([-1.0, 1.0], size=s[1]).astype(np.float32), device="cuda") for s in shapes]
+    Wd = [W.clone().requires_grad_(True) for W in Ws]
+    outs = bcjr_mod.bcjr_quantize_experts(Wd, sl, sr, cb, Ts, L=12, k=2, V=1)
+    gs = [torch.randn(s, device="cuda", generator=torch.Generator("cuda").manual_seed(seed)) for s in shapes]
+    sum((o * g).sum() for o, g in zip(outs, gs)).backward()
+    for e in range(len(shapes)):
+        W1 = Ws[e].clone().requires_grad_(True)
+        ref = bcjr_mod.bcjr_quantize_weight(W1, sl[e], sr[e], cb, Ts[e], L=12, k=2, V=1)
+        (ref * gs[e]).sum().backward()
+        assert (outs[e] - ref).abs().max() <= SOFT_TOL * ref.abs().max(), e
+        assert (Wd[e].grad - W1.grad).abs().max() <= GRAD_TOL * W1.grad.abs().max(), e
