@@ -446,13 +446,12 @@ int bcjr_forward(const bcjr_problem* prob, const float* seq, const float* T, con
                  float* soft, float* logZ, void* ws, size_t ws_bytes, hipStream_t stream) {
   int rc0 = check_ws(prob, OP_FWD, ws, ws_bytes);
   if (rc0 || prob->B == 0) return rc0;
-  Plan pl;
-  int rc = make_plan(prob, OP_FWD, &pl);
-  if (rc) return rc;
-  if (prob->B == 0) return BCJR_OK;
   if (!seq || !T || !soft || !ws) return fail(BCJR_EINVAL, "seq, T, soft and ws must be non-NULL");
   if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
     return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  Plan pl;
+  int rc = make_plan(prob, OP_FWD, &pl);
+  if (rc) return rc;
   bcjr::FwdParams P = {};
   P.seq = seq;
   P.T = T;
@@ -488,14 +487,13 @@ int bcjr_forward_internals(const bcjr_problem* prob, const float* seq, const flo
                            float* log_alpha, float* log_beta, void* ws, size_t ws_bytes, hipStream_t stream) {
   int rc0 = check_ws(prob, OP_FWD, ws, ws_bytes);
   if (rc0 || prob->B == 0) return rc0;
-  Plan pl;
-  int rc = make_plan(prob, OP_FWD_INTERNALS, &pl);
-  if (rc) return rc;
-  if (prob->B == 0) return BCJR_OK;
   if (!seq || !T || !soft || !ws || !marginals || !log_alpha || !log_beta)
     return fail(BCJR_EINVAL, "seq, T, soft, ws, marginals, log_alpha and log_beta must be non-NULL");
   if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
     return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  Plan pl;
+  int rc = make_plan(prob, OP_FWD_INTERNALS, &pl);
+  if (rc) return rc;
   bcjr::FwdParams P = {};
   P.seq = seq;
   P.T = T;
@@ -519,14 +517,13 @@ int bcjr_forward_entropy(const bcjr_problem* prob, const float* seq, const float
                          size_t ws_bytes, hipStream_t stream) {
   int rc0 = check_ws(prob, OP_FWD, ws, ws_bytes);
   if (rc0 || prob->B == 0) return rc0;
-  Plan pl;
-  int rc = make_plan(prob, OP_FWD_INTERNALS, &pl);
-  if (rc) return rc;
-  if (prob->B == 0) return BCJR_OK;
   if (!seq || !T || !soft || !ws || !entropy)
     return fail(BCJR_EINVAL, "seq, T, soft, ws and entropy must be non-NULL");
   if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
     return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  Plan pl;
+  int rc = make_plan(prob, OP_FWD_INTERNALS, &pl);
+  if (rc) return rc;
   bcjr::FwdParams P = {};
   P.seq = seq;
   P.T = T;
@@ -549,14 +546,13 @@ int bcjr_backward(const bcjr_problem* prob, const float* seq, const float* T, co
   (void)logZ;
   int rc0 = check_ws(prob, OP_BWD, ws, ws_bytes);
   if (rc0 || prob->B == 0) return rc0;
-  Plan pl;
-  int rc = make_plan(prob, OP_BWD, &pl);
-  if (rc) return rc;
-  if (prob->B == 0) return BCJR_OK;
   if (!seq || !T || !g_soft || !g_seq || !ws)
     return fail(BCJR_EINVAL, "seq, T, g_soft, g_seq and ws must be non-NULL");
   if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
     return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
+  Plan pl;
+  int rc = make_plan(prob, OP_BWD, &pl);
+  if (rc) return rc;
   bcjr::BwdParams P = {};
   P.seq = seq;
   P.T = T;
@@ -579,14 +575,13 @@ int bcjr_viterbi(const bcjr_problem* prob, const float* seq, const float* codebo
                  size_t ws_bytes, hipStream_t stream) {
   int rc0 = check_ws(prob, OP_VIT, ws, ws_bytes);
   if (rc0 || prob->B == 0) return rc0;
-  Plan pl;
-  int rc = make_plan(prob, OP_VIT, &pl);
-  if (rc) return rc;
-  if (prob->B == 0) return BCJR_OK;
   if (!seq || !ws) return fail(BCJR_EINVAL, "seq and ws must be non-NULL");
   if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
     return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
-  if (packed && 8 % pl.KV != 0) return fail(BCJR_EINVAL, "packing needs k*V to divide 8");
+  if (packed && 8 % (prob->k * prob->V) != 0) return fail(BCJR_EINVAL, "packing needs k*V to divide 8");
+  Plan pl;
+  int rc = make_plan(prob, OP_VIT, &pl);
+  if (rc) return rc;
   bcjr::VitParams P = {};
   P.seq = seq;
   P.table = codebook_or_lut;
@@ -610,17 +605,16 @@ int bcjr_viterbi_constrained(const bcjr_problem* prob, const float* seq, const f
                              size_t ws_bytes, hipStream_t stream) {
   int rc0 = check_ws(prob, OP_VIT, ws, ws_bytes);
   if (rc0 || prob->B == 0) return rc0;
-  Plan pl;
-  int rc = make_plan(prob, OP_VIT, &pl);
-  if (rc) return rc;
-  if (overlap_bits < 0 || overlap_bits > prob->L - pl.KV)
+  if (overlap_bits < 0 || overlap_bits > prob->L - prob->k * prob->V)
     return fail(BCJR_EINVAL, "overlap_bits=%d must lie in [0, L - k*V] = [0, %d]", overlap_bits,
-                prob->L - pl.KV);
-  if (prob->B == 0) return BCJR_OK;
+                prob->L - prob->k * prob->V);
   if (!seq || !ws || !overlap) return fail(BCJR_EINVAL, "seq, overlap and ws must be non-NULL");
   if (prob->code != BCJR_CODE_1MAD && prob->code != BCJR_CODE_3INST && !codebook_or_lut)
     return fail(BCJR_EINVAL, "code %d needs a codebook/LUT pointer", prob->code);
-  if (packed && 8 % pl.KV != 0) return fail(BCJR_EINVAL, "packing needs k*V to divide 8");
+  if (packed && 8 % (prob->k * prob->V) != 0) return fail(BCJR_EINVAL, "packing needs k*V to divide 8");
+  Plan pl;
+  int rc = make_plan(prob, OP_VIT, &pl);
+  if (rc) return rc;
   bcjr::VitParams P = {};
   P.seq = seq;
   P.table = codebook_or_lut;

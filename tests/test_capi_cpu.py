@@ -269,6 +269,45 @@ def test_undersized_workspace_is_reported_before_any_device_call(lib, op):
     assert f"({slot} bytes)" in msg and "100 bytes" in msg
 
 
+@pytest.mark.parametrize("op", ["forward", "forward_entropy", "backward", "viterbi", "viterbi_constrained"])
+def test_missing_pointers_are_reported_before_any_device_call(lib, op):
+    """A null input or output, a table code without its table, an unsupported
+    k*V or an overlap wider than L - k*V: refused on the host, before the launch
+    plan queries the device."""
+    import bcjr._lib as BL
+    d = ctypes.c_void_p(4096)
+    big = 1 << 40
+    p = BL.Problem(16, 2, 1, 4, 256, 0, 9, 0)  # table code
+    if op == "forward":
+        calls = [(lambda: lib.bcjr_forward(ctypes.byref(p), None, d, d, d, None, d, big, None), "non-NULL"),
+                 (lambda: lib.bcjr_forward(ctypes.byref(p), d, d, None, d, None, d, big, None), "codebook")]
+    elif op == "forward_entropy":
+        calls = [(lambda: lib.bcjr_forward_entropy(ctypes.byref(p), d, d, d, d, None, None, d, big, None),
+                  "non-NULL")]
+    elif op == "backward":
+        calls = [(lambda: lib.bcjr_backward(ctypes.byref(p), d, d, d, None, None, None, d, d, big, None),
+                  "non-NULL"),
+                 (lambda: lib.bcjr_backward(ctypes.byref(p), d, d, None, None, d, None, d, d, big, None),
+                  "codebook")]
+    elif op == "viterbi":
+        p3 = BL.Problem(12, 3, 1, 4, 64, 0, 9, 0)
+        calls = [(lambda: lib.bcjr_viterbi(ctypes.byref(p), None, d, None, None, None, None, None, None, d, big,
+                                           None), "non-NULL"),
+                 (lambda: lib.bcjr_viterbi(ctypes.byref(p), d, None, None, None, None, None, None, None, d, big,
+                                           None), "codebook"),
+                 (lambda: lib.bcjr_viterbi(ctypes.byref(p3), d, d, None, None, None, None, None, d, d, big, None),
+                  "k*V=3")]
+    else:
+        calls = [(lambda: lib.bcjr_viterbi_constrained(ctypes.byref(p), d, d, 15, d, None, None, None, None, None,
+                                                       None, d, big, None), "overlap_bits=15"),
+                 (lambda: lib.bcjr_viterbi_constrained(ctypes.byref(p), d, d, 4, None, None, None, None, None,
+                                                       None, None, d, big, None), "non-NULL")]
+    for call, msg in calls:
+        rc = call()
+        assert rc in (BL.BCJR_EINVAL, BL.BCJR_EUNSUPPORTED), (rc, lib.bcjr_last_error())
+        assert msg in lib.bcjr_last_error().decode()
+
+
 def test_viterbi_trace_validates_before_any_device_call(lib):
     """bcjr_viterbi_trace refuses bad problems and missing pointers on the host
     (no device needed), and an empty batch is a no-op."""
