@@ -84,7 +84,7 @@ enum {
 };
 
 /* Problem description.  kV = k * V bits per step must be 1, 2 or 4, and
- * 2*kV <= L <= 16 (kV = 1 requires L <= 11). */
+ * 2*kV <= L <= 16 (kV = 1 requires L <= 11 and the table code). */
 typedef struct {
     int L;          /* state bits: S = 2^L states                          */
     int k;          /* bits per weight                                     */

@@ -87,6 +87,8 @@ int validate(const bcjr_problem* p) {
   if (p->L < 2 * KV || p->L > 16)
     return fail(BCJR_EUNSUPPORTED, "L=%d outside [%d, 16] for k*V=%d", p->L, 2 * KV, KV);
   if (KV == 1 && p->L > 11) return fail(BCJR_EUNSUPPORTED, "k*V=1 supports L <= 11 (got %d)", p->L);
+  if (KV == 1 && p->code != BCJR_CODE_TABLE)
+    return fail(BCJR_EUNSUPPORTED, "k*V=1 is built for the table code only (got code %d)", p->code);
   if (p->B < 0) return fail(BCJR_EINVAL, "B=%lld must be >= 0", (long long)p->B);
   if (p->N < 1 || p->N > 4096) return fail(BCJR_EINVAL, "N=%lld outside [1, 4096]", (long long)p->N);
   switch (p->code) {
@@ -298,6 +300,9 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
       const bool cache_w = (pl->NSUB == 1) && (upt_w * R * R * p->V <= 64);
       const int wcode = cache_w ? p->code : kcode;
       const void* fn_w = bcjr::vit_kernel_ptr(KV, p->V, wcode, upt_w, cache_w, true);
+      // ... and its LDS fits (the HYB LUT copies of the uncached instances do
+      // not beside a 2^14-state cost vector: k = 1, V = 2 at L = 16).
+      if (fn_w && bcjr::vit_lds_bytes(p->L, KV, p->V, N, 16, wcode, p->Q, !cache_w) > di.max_lds) fn_w = nullptr;
       if (fn_w) {
         vcode = wcode;
         pl->fn = fn_w;

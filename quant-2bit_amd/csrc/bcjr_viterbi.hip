@@ -781,6 +781,7 @@ const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache, bool wi
   BCJR_VIT_CASE(2, 2, CODE_HYB, 1, true)
   BCJR_VIT_CASE(2, 2, CODE_HYB, 2, true)
   BCJR_VIT_CASE(2, 2, CODE_HYB, 4, true)
+  BCJR_VIT_CASE(2, 2, CODE_HYB, 8, false)  // L = 16, k = 1: one plain LUT copy
   BCJR_VIT_CASE(4, 1, CODE_TABLE, 1, false)
   BCJR_VIT_CASE(4, 1, CODE_TABLE, 2, false)
   BCJR_VIT_CASE(4, 1, CODE_1MAD, 1, false)
@@ -798,6 +799,10 @@ const void* vit_kernel_ptr(int KV, int V, int code, int upt, bool cache, bool wi
   BCJR_VIT_WIDE(2, 2, CODE_TABLE, 2, true)
   BCJR_VIT_WIDE(2, 2, CODE_HYB, 1, true)
   BCJR_VIT_WIDE(2, 2, CODE_HYB, 2, true)
+  // k = 1, V = 2 at L = 16: 4 butterflies per thread, whose 128 codewords do not
+  // fit the cache, so they are read per state.
+  BCJR_VIT_WIDE(2, 2, CODE_TABLE, 4, false)
+  BCJR_VIT_WIDE(2, 2, CODE_HYB, 4, false)
   BCJR_VIT_WIDE(4, 1, CODE_TABLE, 1, false)
   BCJR_VIT_WIDE(4, 1, CODE_1MAD, 1, false)
   BCJR_VIT_WIDE(4, 1, CODE_3INST, 1, false)

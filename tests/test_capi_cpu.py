@@ -57,6 +57,7 @@ def test_strerror_and_version(lib):
     (17, 2, 1, 0, 9, 4, 256, -2, "L=17"),
     (3, 2, 1, 0, 9, 4, 256, -2, "L=3"),
     (12, 1, 1, 0, 9, 4, 256, -2, "k*V=1 supports L <= 11"),
+    (10, 1, 1, 2, 9, 4, 256, -2, "table code only"),
     (16, 2, 3, 0, 9, 4, 256, -1, "V=3"),
     (16, 2, 1, 0, 9, -1, 256, -1, "B=-1"),
     (16, 2, 1, 0, 9, 4, 0, -1, "N=0"),

@@ -455,6 +455,8 @@ VIT_CASES = [  # (L, k, V, N, B, kind)
     (16, 2, 2, 128, 2, "hyb"),         # 1024 threads, 16 interleaved LUT copies
     (15, 1, 2, 64, 2, "hyb"),          # 1024 threads, cached codewords, 2 butterflies per thread
     (14, 2, 1, 128, 3, "3inst"),       # 1024 threads, one butterfly per thread
+    (16, 1, 2, 64, 2, "table"),        # 1024 threads, 4 uncached butterflies per thread
+    (16, 1, 2, 64, 2, "hyb"),          # 512 threads, one LUT copy (the copies do not fit beside 2^14 states)
 ]
 
 

@@ -291,3 +291,89 @@ def test_experts_sweep_vs_per_weight_loop(bcjr_mod, seed):
         (ref * gs[e]).sum().backward()
         assert (outs[e] - ref).abs().max() <= SOFT_TOL * ref.abs().max(), e
         assert (Wd[e].grad - W1.grad).abs().max() <= GRAD_TOL * W1.grad.abs().max(), e
+
+
+def _ste_cases(n=12, seed=19):
+    """(m, n, L, k, V, kind, packed): a weight through the hard quantizer, then
+    stored, loaded and dequantized."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        m, nn = 1 << int(rng.integers(4, 10)), 1 << int(rng.integers(4, 10))
+        if m * nn > 65536:
+            continue
+        k, V = [(2, 1), (1, 2), (2, 2), (1, 1)][int(rng.integers(4))]
+        kV = k * V
+        L = int(rng.integers(max(2 * kV, 6), (11 if kV == 1 else 16) + 1))
+        kinds = ["table"] + (["1mad", "3inst"] if V == 1 else ["hyb"])
+        out.append((m, nn, L, k, V, kinds[int(rng.integers(len(kinds)))], bool(rng.integers(2))))
+    return out
+
+
+@pytest.mark.parametrize("m,n,L,k,V,kind,packed", _ste_cases())
+def test_ste_and_round_trip_sweep(bcjr_mod, oracle, m, n, L, k, V, kind, packed, tmp_path):
+    """quantize_forward_gpu (RHT, RMS scale, tiles, Viterbi, back) against the
+    oracle's Viterbi composed with the same steps (bit-exact where m*n is an even
+    power of two, else within the inverse RHT's scale rounding), then save (uint8
+    or packed file) -> load -> dequantize equal to it bit for bit."""
+    import bcjr
+    from bcjr.quant import tile_for_viterbi, untile_from_viterbi
+    print(f"ste sweep {m}x{n} L={L} k={k} V={V} {kind} packed={packed}", flush=True)
+    rng = np.random.default_rng(m * 17 + n * 3 + L)
+    cb, cb_np = _codebook(bcjr_mod, kind, L, V, rng)
+    sl = torch.tensor(rng.choice([-1.0, 1.0], size=m).astype(np.float32), device="cuda")
+    sr = torch.tensor(rng.choice([-1.0, 1.0], size=n).astype(np.float32), device="cuda")
+    W = torch.tensor((rng.standard_normal((m, n)) * 0.03).astype(np.float32), device="cuda")
+    Wq = bcjr.quantize_forward_gpu(W, sl, sr, cb, k=k)
+
+    Wt = bcjr.apply_rht_gpu(W, sl, sr)
+    s = Wt.pow(2).mean().sqrt().clamp(min=1e-30)
+    seqs, info = tile_for_viterbi((Wt / s).cpu(), 16, 16)
+    walk_r, bits_r, start_r, recon_r, _ = oracle.viterbi(seqs.numpy().reshape(seqs.shape[0], -1, V), cb_np, L, k * V)
+    Wtq = untile_from_viterbi(torch.tensor(recon_r.reshape(seqs.shape[0], -1)), info, (m, n), 16, 16)
+    ref = oracle.inverse_rht((Wtq * s.cpu()).numpy(), sl.cpu().numpy(), sr.cpu().numpy())
+    if ((m * n).bit_length() - 1) % 2 == 0:  # 1/sqrt(mn) exact
+        assert np.array_equal(Wq.cpu().numpy(), ref)
+    else:
+        assert np.abs(Wq.cpu().numpy() - ref).max() <= 2 * np.spacing(np.abs(ref).max())
+
+    nr, nc = info
+    args = dict(bitstreams=bits_r.reshape(nc, nr, -1).astype(np.uint8), start_states=start_r.reshape(nc, nr),
+                sign_l=sl.cpu().numpy(), sign_r=sr.cpu().numpy(), W_scale=float(s), shape=(m, n),
+                meta={"layer": 0, "kind": "mlp", "proj": kind},
+                config={"L": L, "k": k, "V": V, "Tx": 16, "Ty": 16})
+    if packed and 8 % (k * V) != 0:
+        packed = False
+    path = str(tmp_path / ("w.safetensors" if packed else "w.pt"))
+    (bcjr.save_packed if packed else bcjr.save_quantized)(path, **args)
+    assert torch.equal(bcjr.dequant_target_gpu(bcjr.load_quantized(path), codebook=cb), Wq)
+
+
+def test_every_accepted_problem_has_a_launch_plan(bcjr_mod):
+    """Every problem the C ABI's validation accepts (each built k*V and V, every
+    L it allows, every code it allows there, HYB at Q = 9 and Q = 10, short and
+    long sequences) gets a launch plan for the forward, the backward and the
+    Viterbi: a kernel instance exists and is resident.  No kernel runs.  A
+    generator code at k*V = 1 is refused by the validation itself."""
+    import ctypes
+    from bcjr import _lib as BL
+    lib = bcjr_mod.load_library()
+    missing = []
+    for k, V in SHAPES:
+        kV = k * V
+        for L in range(2 * kV, (11 if kV == 1 else 16) + 1):
+            codes = [(BL.CODE_TABLE, 9)]
+            if kV > 1:  # k*V = 1 is built for the table code only
+                codes += [(BL.CODE_1MAD, 9), (BL.CODE_3INST, 9)] if V == 1 else [(BL.CODE_HYB, 9), (BL.CODE_HYB, 10)]
+            for code, Q in codes:
+                for N in (1, 256):
+                    for op in (BL.OP_FORWARD, BL.OP_BACKWARD, BL.OP_VITERBI):
+                        p = BL.Problem(L, k, V, 4, N, code, Q, 0)
+                        n = ctypes.c_size_t(0)
+                        if lib.bcjr_workspace_bytes(ctypes.byref(p), op, ctypes.byref(n)) != 0 or n.value == 0:
+                            missing.append((L, k, V, code, Q, N, op, lib.bcjr_last_error().decode()))
+    assert not missing, "\n".join(map(str, missing[:40]))
+    p = BL.Problem(8, 1, 1, 4, 16, BL.CODE_3INST, 9, 0)
+    assert lib.bcjr_workspace_bytes(ctypes.byref(p), BL.OP_FORWARD, ctypes.byref(ctypes.c_size_t(0))) == \
+        BL.BCJR_EUNSUPPORTED
+    assert "table code only" in lib.bcjr_last_error().decode()
