@@ -377,3 +377,55 @@ def test_every_accepted_problem_has_a_launch_plan(bcjr_mod):
     assert lib.bcjr_workspace_bytes(ctypes.byref(p), BL.OP_FORWARD, ctypes.byref(ctypes.c_size_t(0))) == \
         BL.BCJR_EUNSUPPORTED
     assert "table code only" in lib.bcjr_last_error().decode()
+
+
+def _diag_cases(n=16, seed=23):
+    """(L, k, V, kind, N, B, T): small trellises for the diagnostics outputs."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        k, V = SHAPES[int(rng.integers(len(SHAPES)))]
+        kV = k * V
+        L = int(rng.integers(2 * kV, 13))
+        kinds = ["table"] + (["1mad", "3inst"] if V == 1 else ["hyb"])
+        kind = kinds[int(rng.integers(len(kinds)))]
+        N = int(rng.choice([1, 2, 5, 16, 33, 48]))
+        T = round(float(np.exp(rng.uniform(np.log(0.1), np.log(1.5)))), 4)
+        out.append((L, k, V, kind, N, int(rng.integers(1, 4)), T))
+    return out
+
+
+@pytest.mark.parametrize("L,k,V,kind,N,B,T", _diag_cases())
+def test_diagnostics_sweep_vs_oracle(bcjr_mod, oracle, L, k, V, kind, N, B, T):
+    """return_internals (P, log alpha, log beta per state) against the gather
+    form of forward_backward.py; the marginal entropy against the oracle; the
+    walk replay from bitstreams and from packed bytes, and the Viterbi trace,
+    bit-exact."""
+    from bcjr import bcjr_forward_backward, viterbi_decode_v_batched, viterbi_encode_v_batched_hip, ops
+    print(f"diagnostics sweep L={L} k={k} V={V} {kind} N={N} B={B} T={T}", flush=True)
+    rng = np.random.default_rng(L * 389 + N * 11 + B)
+    cb, cb_np = _codebook(bcjr_mod, kind, L, V, rng)
+    seq = _weights(rng, (B, N, V), tails=False)
+    x = torch.tensor(seq, device="cuda")
+    soft, logZ, P, la, lb = bcjr_forward_backward(x, cb, T, L=L, k=k, V=V, return_internals=True)
+    s2, z2, P2, la2, lb2 = oracle.naive_forward(seq, cb_np, T, L, k * V, return_internals=True)
+    assert max_rel(soft.detach().cpu().numpy(), s2) < SOFT_TOL
+    assert np.abs(P.cpu().numpy() - P2).max() < 1e-5
+    assert np.abs(la.cpu().numpy() - la2).max() < 1e-4 * max(1.0, np.abs(la2).max())
+    assert np.abs(lb.cpu().numpy() - lb2).max() < 1e-4 * max(1.0, np.abs(lb2).max())
+    H = bcjr_mod.bcjr_marginal_entropy(x, cb, T, L=L, k=k, V=V).cpu().numpy().astype(np.float64)
+    H_ref = oracle.marginal_entropy(seq, cb_np, T, L, k * V)
+    assert np.abs(H - H_ref).max() <= 1e-4 * max(1.0, float(np.abs(H_ref).max()))
+
+    bits, start, recon, mse, out = viterbi_encode_v_batched_hip(x.reshape(B, N * V), cb, L=L, k=k, V=V,
+                                                                return_all=True)
+    w1, r1 = viterbi_decode_v_batched(bits, start, cb, L=L, k=k, V=V)
+    assert torch.equal(w1, out["walk"]) and torch.equal(r1, recon)
+    if out["packed"] is not None:
+        w2, r2 = viterbi_decode_v_batched(None, start, cb, L=L, k=k, V=V, packed=out["packed"], N=N)
+        assert torch.equal(w2, out["walk"]) and torch.equal(r2, recon)
+    tr, bp = ops.viterbi_trace(ops.Spec(L, k, V, ops.CODE_TABLE), x, cb)
+    for b in range(B):
+        t_r, b_r = oracle.viterbi_trace(seq[b], cb_np, L, k * V)
+        assert np.array_equal(tr[b].cpu().numpy(), t_r)
+        assert np.array_equal(bp[b].cpu().numpy(), b_r)
