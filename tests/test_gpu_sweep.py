@@ -429,3 +429,39 @@ def test_diagnostics_sweep_vs_oracle(bcjr_mod, oracle, L, k, V, kind, N, B, T):
         t_r, b_r = oracle.viterbi_trace(seq[b], cb_np, L, k * V)
         assert np.array_equal(tr[b].cpu().numpy(), t_r)
         assert np.array_equal(bp[b].cpu().numpy(), b_r)
+
+
+def test_calls_on_two_streams_overlap_safely(bcjr_mod):
+    """Forward, backward and Viterbi of two independent batches issued on two
+    streams (default priority) at once, each with its own workspace from the
+    caching allocator of its stream: every output equals the same call made
+    alone, bit for bit."""
+    from bcjr import ops
+    cb = bcjr_mod.make_3inst_codebook(14, "cuda")
+    spec, table = bcjr_mod.codes.resolve_codebook(cb, 14, 2, 1, torch.device("cuda"))
+    gen = torch.Generator("cuda").manual_seed(5)
+    xs = [torch.randn(600, 64, 1, device="cuda", generator=gen) for _ in range(2)]
+    gs = [torch.randn(600, 64, 1, device="cuda", generator=gen) for _ in range(2)]
+    Ts = [0.1, 0.3]
+    alone = []
+    for x, g, T in zip(xs, gs, Ts):
+        soft, logZ = ops.forward(spec, x, T, table)
+        d = ops.backward(spec, x, T, table, g)
+        v = ops.viterbi(spec, x, table)
+        alone.append((soft, logZ, d, v["walk"], v["recon"]))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    both = [None, None]
+    for _ in range(2):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                soft, logZ = ops.forward(spec, xs[i], Ts[i], table)
+                d = ops.backward(spec, xs[i], Ts[i], table, gs[i])
+                v = ops.viterbi(spec, xs[i], table)
+                both[i] = (soft, logZ, d, v["walk"], v["recon"])
+        torch.cuda.synchronize()
+        for i in range(2):
+            for got, ref in zip(both[i], alone[i]):
+                assert torch.equal(got, ref)
