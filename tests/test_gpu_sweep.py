@@ -465,3 +465,62 @@ def test_calls_on_two_streams_overlap_safely(bcjr_mod):
         for i in range(2):
             for got, ref in zip(both[i], alone[i]):
                 assert torch.equal(got, ref)
+
+
+def _max_N(lib, BL, L, k, V, code, op):
+    """Longest sequence the launch plan accepts (LDS-bound), by bisection."""
+    import ctypes
+    lo, hi = 1, 4096
+    def ok(N):
+        p = BL.Problem(L, k, V, 1, N, code, 9, 0)
+        return lib.bcjr_workspace_bytes(ctypes.byref(p), op, ctypes.byref(ctypes.c_size_t(0))) == 0
+    assert ok(lo)
+    if ok(hi):
+        return hi
+    while hi - lo > 1:
+        mid = (lo + hi) // 2
+        lo, hi = (mid, hi) if ok(mid) else (lo, mid)
+    return lo
+
+
+@pytest.mark.parametrize("L,k,V,kind", [(16, 2, 2, "hyb"), (16, 2, 2, "table"), (16, 1, 2, "hyb"),
+                                        (11, 1, 1, "table"), (12, 2, 1, "1mad"), (16, 4, 1, "3inst")])
+def test_longest_sequence_per_shape_vs_oracle(bcjr_mod, oracle, L, k, V, kind):
+    """At each shape's longest accepted sequence (the LDS bound of its launch
+    plan, or N = 4096): forward, gradient and Viterbi against the oracle, and
+    one step more refused before any launch."""
+    from bcjr import _lib as BL, bcjr_forward_backward, ops, viterbi_encode_v_batched_hip
+    lib = bcjr_mod.load_library()
+    rng = np.random.default_rng(L * 31 + k * 7 + V)
+    cb, cb_np = _codebook(bcjr_mod, kind, L, V, rng)
+    spec, table = bcjr_mod.codes.resolve_codebook(cb, L, k, V, torch.device("cuda"))
+    limits = {op: _max_N(lib, BL, L, k, V, spec.code, op) for op in (BL.OP_FORWARD, BL.OP_BACKWARD, BL.OP_VITERBI)}
+    print(f"longest L={L} k={k} V={V} {kind}: forward, backward, Viterbi {list(limits.values())}", flush=True)
+    # N = 4096 is the ABI's own cap, not an LDS bound: a shorter sequence keeps the oracle quick there
+    Nf, Nb, Nv = (n if n < 4096 else 1024 for n in limits.values())
+    T = 0.2
+    N = min(Nf, Nb)
+    seq = rng.standard_normal((1, N, V)).astype(np.float32)
+    g = rng.standard_normal((1, N, V)).astype(np.float32)
+    x = torch.tensor(seq, device="cuda", requires_grad=True)
+    soft, logZ = bcjr_forward_backward(x, cb, T, L=L, k=k, V=V)
+    (soft * torch.tensor(g, device="cuda")).sum().backward()
+    s_ref, z_ref = oracle.bcjr_forward(seq, cb_np, T, L, k * V)
+    assert max_rel(soft.detach().cpu().numpy(), s_ref) < SOFT_TOL
+    assert max_rel(x.grad.cpu().numpy(), oracle.bcjr_backward(seq, cb_np, T, L, k * V, g)) < GRAD_TOL
+    if Nf > N:
+        seq_f = rng.standard_normal((1, Nf, V)).astype(np.float32)
+        soft_f, _ = ops.forward(spec, torch.tensor(seq_f, device="cuda"), T, table)
+        assert max_rel(soft_f.cpu().numpy(), oracle.bcjr_forward(seq_f, cb_np, T, L, k * V)[0]) < SOFT_TOL
+    seq_v = rng.standard_normal((1, Nv, V)).astype(np.float32)
+    bits, start, recon, mse, out = viterbi_encode_v_batched_hip(torch.tensor(seq_v.reshape(1, -1), device="cuda"),
+                                                                cb, L=L, k=k, V=V, return_all=True)
+    assert np.array_equal(out["walk"].cpu().numpy(), oracle.viterbi(seq_v, cb_np, L, k * V)[0])
+    for op, N_over in limits.items():
+        if N_over < 4096:  # an LDS bound
+            import ctypes
+            p = BL.Problem(L, k, V, 1, N_over + 1, spec.code, 9, 0)
+            assert lib.bcjr_workspace_bytes(ctypes.byref(p), op, ctypes.byref(ctypes.c_size_t(0))) == \
+                BL.BCJR_EUNSUPPORTED
+            assert "LDS" in lib.bcjr_last_error().decode()
+
