@@ -33,7 +33,9 @@ def cosine_temperature_schedule(step, total_steps, T_0, T_min):
 
 
 def bcjr_marginal_entropy(sequences, codebook, T_temp, L=L_BITS, k=K_BITS, V=V_DIM):
-    """Marginal entropy H[b, t] = -sum_s P_t(s) ln P_t(s) in nats, (B, N) float32.
+    """Marginal entropy H[b, t] = -sum_s P_t(s) ln P_t(s) in nats, (B, N) float32: what
+    src/bcjr/anneal.py:143-184 (entropy_diagnostic) reduces from the (B, N, 2^L)
+    marginals of return_internals=True, here fused into the forward.
 
     Same arguments as bcjr_forward_backward (T_temp may be per sequence); no
     gradient.  Bounds: 0 <= H <= L ln 2, the upper one reached by the uniform

@@ -37,12 +37,14 @@ def _tag(cb: torch.Tensor, code: int, lut=None, Q: int = 9) -> torch.Tensor:
 
 
 def make_1mad_codebook(L: int = 16, device="cuda") -> torch.Tensor:
-    """(2^L, 1): ((byte sum of 34038481*s + 76625530) - 510) / 147.8."""
+    """(2^L, 1): ((byte sum of 34038481*s + 76625530) - 510) / 147.8, the table of
+    src/codes/ref.py:33-41 (decode_1mad_batch), hashed on the device."""
     return _tag(ops.codebook(CODE_1MAD, L, device), CODE_1MAD)
 
 
 def make_3inst_codebook(L: int = 16, device="cuda") -> torch.Tensor:
-    """(2^L, 1): fp16-pair sum of (89226354*s + 64248484) & 0x8FFF8FFF ^ fp16(0.922), / 1.2447."""
+    """(2^L, 1): fp16-pair sum of (89226354*s + 64248484) & 0x8FFF8FFF ^ fp16(0.922), / 1.2447,
+    the table of src/codes/ref.py:76-91 (decode_3inst_batch), hashed on the device."""
     return _tag(ops.codebook(CODE_3INST, L, device), CODE_3INST)
 
 

@@ -46,7 +46,9 @@ def _per_weight_T(T_temps, E, device):
 
 def bcjr_quantize_experts(W_latents, sign_l, sign_r, codebook, T_temps, Tx=TX, Ty=TY,
                           L=L_BITS, k=K_BITS, V=V_DIM):
-    """Soft-quantize E weights in one engine call.
+    """Soft-quantize E weights in one engine call, in place of one
+    bcjr_quantize_weight per expert weight (src/qat/qat_moe_layer.py:106-114 loops
+    the experts).
 
     W_latents: sequence of E float32 GPU tensors (m_e, n_e) (gradients allowed),
                m_e, n_e powers of two divisible by Tx, Ty.

@@ -70,7 +70,9 @@ hadamard_op.register_autograd(_hadamard_backward, setup_context=_hadamard_setup)
 
 
 def hadamard_transform(x: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
-    """scale * H_n x along the last axis (unscaled Sylvester H_n, n a power of two)."""
+    """scale * H_n x along the last axis (unscaled Sylvester H_n, n a power of two): the
+    fast_hadamard_transform call of src/qat/ste.py:113-135, with the butterflies of
+    src/rht/transform.py:26-42 (fwht_numpy)."""
     return hadamard_op(x, float(scale))
 
 
@@ -160,12 +162,14 @@ rht_batched_op.register_autograd(_rht_batched_backward, setup_context=_rht_setup
 
 
 def apply_rht_batched(W, sign_l, sign_r):
-    """apply_rht_gpu on each matrix of W (E, m, n), signs (E, m) and (E, n)."""
+    """apply_rht_gpu (src/rht/transform.py:65-97) on each matrix of W (E, m, n),
+    signs (E, m) and (E, n)."""
     return rht_batched_op(W, sign_l, sign_r, False)
 
 
 def apply_inverse_rht_batched(W_tilde, sign_l, sign_r):
-    """apply_inverse_rht_gpu on each matrix of W_tilde (E, m, n)."""
+    """apply_inverse_rht_gpu (src/rht/transform.py:100-126) on each matrix of
+    W_tilde (E, m, n)."""
     return rht_batched_op(W_tilde, sign_l, sign_r, True)
 
 

@@ -215,7 +215,7 @@ def _codebook_source(L, k, V, codebook=None, decode_fn=None, device="cuda"):
 
 def dequant_target_gpu(saved, codebook=None, decode_fn=None, device="cuda", rotated=False):
     """Dequantized weight (m, n) float32 on `device` from a payload of either
-    kind.  rotated=True stops before the inverse RHT (the rotated-basis matrix
+    kind (src/quantize/serialize.py:55-107 dequant_target, on the GPU).  rotated=True stops before the inverse RHT (the rotated-basis matrix
     W_unit * W_scale that in-place QAT trains)."""
     device = torch.device(device)
     cfg = saved["config"]

@@ -17,7 +17,10 @@ from .codes import resolve_codebook
 
 
 def viterbi_encode_v_batched_hip(sequences, codebook, L=16, k=2, V=2, return_all=False):
-    """sequences: (B, T) float32 with T = N*V; codebook (2^L, V).
+    """Batched Viterbi (src/viterbi/cuda_kernel.py:166-220 viterbi_encode_v_batched_cuda,
+    src/viterbi/encode.py:425-495 viterbi_encode_v_batched) for any L, k, V.
+
+    sequences: (B, T) float32 with T = N*V; codebook (2^L, V).
 
     Returns (bitstreams (B, N) int32, start_states (B,) int32,
     recons (B, T) float32, mses (B,) float32); with return_all also the dict
@@ -120,7 +123,9 @@ def viterbi_encode_chunked(sequences, codebook, chunk=None, L=16, k=2, V=2):
 
 
 def viterbi_decode_v_batched(bitstreams, start_states, codebook, L=16, k=2, V=2, packed=None, N=None):
-    """Replay walks: returns (walks (B, N) int32, recons (B, N*V) float32)."""
+    """Replay walks (src/viterbi/encode.py:310-325 viterbi_decode_v, batched as
+    src/qat/ste.py:270-283 _replay_walks): returns (walks (B, N) int32, recons
+    (B, N*V) float32)."""
     spec, table = resolve_codebook(codebook, L, k, V, start_states.device)
     walk, recon = ops.decode(spec, start_states, table, bitstream=bitstreams, packed=packed, N=N)
     return walk, recon.reshape(walk.shape[0], -1)
