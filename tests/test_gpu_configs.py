@@ -18,8 +18,9 @@ Workloads (L=16, k=2, V=1, 3INST, 256 weights per sequence):
     alternating across the exact / group-sum variants within each workgroup;
   * the MLP block (gate/up/down at full shape, per-row lognormal scales)
     through bcjr_quantize_weight (RHT, RMS scale, tiles, node, inverse RHT);
-  * OLMoE-1B-7B experts (gate/up 1024x2048, down 2048x1024, lognormal
-    per-expert scales, T = 0.1) through bcjr_quantize_experts.
+  * the OLMoE-1B-7B MoE layer whole: 64 experts (gate/up 1024x2048, down
+    2048x1024, lognormal per-expert scales, T = 0.1, 1,572,864 sequences)
+    through one bcjr_quantize_experts call.
 """
 import ctypes
 import sys
@@ -216,26 +217,56 @@ def test_llama_mlp_block_full_shape(bcjr_mod, oracle, cb3):
                            [0, B // 3, B - 1], f"mlp {name}")
 
 
-def test_olmoe_experts_full_shape(bcjr_mod, oracle, cb3):
-    """4 OLMoE-1B-7B experts (gate/up 1024x2048, down 2048x1024) with lognormal
-    per-expert scales (sigma 0.5, seed 0), every weight in one
-    bcjr_quantize_experts call at T = 0.1, one backward."""
+def test_olmoe_64_experts_whole_layer(bcjr_mod, oracle, cb3):
+    """The OLMoE-1B-7B MoE layer whole: 64 experts, each gate/up 1024x2048 and
+    down 2048x1024 (192 weights, 402,653,184 weights, 1,572,864 sequences),
+    N(0,1) weights times a lognormal (sigma 0.5, seed 0) per-expert scale, every
+    weight in ONE bcjr_quantize_experts call at T = 0.1 (one forward and one
+    backward launch over all 1,572,864 sequences), where the reference loops the
+    experts (src/qat/qat_moe_layer.py:106-114).  Every output: finite, the
+    gradient finite, and every soft tile (read back through the orthogonal RHT of
+    W_q) inside the codebook's hull.  The first and last tile of seven weights
+    (gate, up and down of the first, a middle and the last expert) against the
+    oracle composition."""
     from bcjr import bcjr_quantize_experts, make_sign_vector
+    from bcjr.quant import tile_for_viterbi
+    from bcjr.rht import apply_rht_batched
     cb, cb_np = cb3
-    E = 4
+    E = 64
     rng = np.random.default_rng(0)
     scales = np.exp(0.5 * rng.standard_normal(E)).astype(np.float32)
     shapes = [(1024, 2048), (1024, 2048), (2048, 1024)] * E
-    Ws = [torch.tensor(rng.standard_normal(s).astype(np.float32) * scales[i // 3], device="cuda",
-                       requires_grad=True) for i, s in enumerate(shapes)]
-    sl = [torch.tensor(make_sign_vector(s[0], 10 + i), device="cuda") for i, s in enumerate(shapes)]
-    sr = [torch.tensor(make_sign_vector(s[1], 50 + i), device="cuda") for i, s in enumerate(shapes)]
-    _say(f"olmoe: {E} experts, {sum(m * n // 256 for m, n in shapes)} sequences")
-    outs = bcjr_quantize_experts(Ws, sl, sr, cb, 0.1, L=L, k=K, V=V)
-    Gs = [torch.randn(s, device="cuda", generator=torch.Generator("cuda").manual_seed(20 + i))
+    gen = torch.Generator("cuda").manual_seed(0)
+    Ws = [(torch.randn(s, device="cuda", generator=gen) * float(scales[i // 3])).requires_grad_(True)
           for i, s in enumerate(shapes)]
+    sl = [torch.tensor(make_sign_vector(s[0], 10 + i), device="cuda") for i, s in enumerate(shapes)]
+    sr = [torch.tensor(make_sign_vector(s[1], 500 + i), device="cuda") for i, s in enumerate(shapes)]
+    seqs = sum(m * n // 256 for m, n in shapes)
+    assert seqs == 1572864
+    _say(f"olmoe: {E} experts, {len(shapes)} weights, {seqs} sequences in one call")
+    outs = bcjr_quantize_experts(Ws, sl, sr, cb, 0.1, L=L, k=K, V=V)
+    Gs = [torch.randn(s, device="cuda", generator=gen) for s in shapes]
     torch.autograd.backward(outs, Gs)
-    for i in (0, 4, 8, 11):  # gate of expert 0, up of expert 1, down of expert 2, down of expert 3
+    torch.cuda.synchronize()
+    _say("olmoe: forward + backward done")
+    lo, hi = float(cb.min()), float(cb.max())
+    slack = 1e-4 * max(abs(lo), abs(hi))  # the RHT round trip adds float32 rounding
+    with torch.no_grad():
+        for shape in ((1024, 2048), (2048, 1024)):
+            idx = [i for i, s in enumerate(shapes) if s == shape]
+            for c0 in range(0, len(idx), 32):
+                part = idx[c0:c0 + 32]
+                Wq = torch.stack([outs[i] for i in part])
+                assert torch.isfinite(Wq).all(), f"olmoe W_q {part[0]}..{part[-1]}"
+                assert all(torch.isfinite(Ws[i].grad).all() for i in part), f"olmoe grad {part[0]}.."
+                SL, SR = torch.stack([sl[i] for i in part]), torch.stack([sr[i] for i in part])
+                Wt = apply_rht_batched(torch.stack([Ws[i].detach() for i in part]), SL, SR)
+                scale = Wt.pow(2).mean(dim=(1, 2)).sqrt()
+                soft_rot = apply_rht_batched(Wq, SL, SR) / scale[:, None, None]
+                assert float(soft_rot.min()) >= lo - slack and float(soft_rot.max()) <= hi + slack, \
+                    f"olmoe hull {part[0]}..{part[-1]}"
+                del Wq, Wt, soft_rot
+    for i in (0, 1, 2, 97, 188, 190, 191):
         B = shapes[i][0] * shapes[i][1] // 256
         _spot_check_weight(bcjr_mod, oracle, cb_np, Ws[i].detach(), sl[i], sr[i], outs[i].detach(), Ws[i].grad,
                            Gs[i], 0.1, [0, B - 1], f"olmoe weight {i}")

@@ -401,3 +401,34 @@ def test_torch_eager_restatement_matches_oracle(oracle):
         s2, _ = eager_bcjr(x, torch.tensor(cb), 0.2, L, kV, checkpoint=False)
         s2.backward(torch.tensor(g))
         assert torch.allclose(s2.detach(), s, rtol=0, atol=1e-6) and torch.allclose(x.grad, d, rtol=0, atol=1e-5)
+
+
+@pytest.mark.parametrize("kV,V,N,code,T", [(2, 1, 256, "3inst", 0.1), (4, 2, 128, "hyb", 0.3)])
+def test_oracle_at_l16_matches_float64_gather_form(oracle, kV, V, N, code, T):
+    """The C oracle at the headline trellis size, L = 16 (65,536 states), one
+    tile, against oracle/torch_ref.py's literal gather form run in float64 (the
+    reference's eager node, src/bcjr/forward_backward.py:89-232, every state
+    gathering its 2^kV predecessors; autograd for the gradient).  kV = 2 with
+    the 3INST code at N = 256 (the layer's trellis) and kV = 4 with a HYB Q = 9
+    table at N = 128 (the reference's QAT trellis).  The two share no code, so
+    an L-dependent mistake in the structure-aware oracle -- a shift or mask
+    width, a reduced-state index, 32-bit index arithmetic over 2^16 x 256 cells
+    -- fails here; the tolerances are the float32 rounding of the oracle's
+    outputs, 100-1000 times tighter than the parity gates."""
+    import torch
+    from oracle.torch_ref import eager_step
+    L = 16
+    rng = np.random.default_rng(16 + kV)
+    seq = rng.standard_normal((1, N, V)).astype(np.float32)
+    g = rng.standard_normal((1, N, V)).astype(np.float32)
+    if code == "hyb":
+        cb = oracle.codebook(oracle.CODE_HYB, L, lut=rng.standard_normal((512, 2)).astype(np.float32), Q=9)
+    else:
+        cb = oracle.codebook(oracle.CODE_3INST, L)
+    f64 = lambda a: torch.tensor(a, dtype=torch.float64)  # noqa: E731
+    s, z, d = eager_step(f64(seq), f64(cb), T, L, kV, f64(g))
+    s_ref, z_ref = oracle.bcjr_forward(seq, cb, T, L, kV)
+    d_ref = oracle.bcjr_backward(seq, cb, T, L, kV, g)
+    assert np.abs(s.numpy() - s_ref).max() <= 1e-6 * np.abs(s_ref).max()
+    assert np.abs(z.numpy() - z_ref).max() <= 1e-6 * np.abs(z_ref).max()
+    assert np.abs(d.numpy() - d_ref).max() <= 1e-5 * np.abs(d_ref).max()
