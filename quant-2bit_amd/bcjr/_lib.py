@@ -1,17 +1,22 @@
-"""ctypes binding of the C ABI in include/bcjr_hip.h (libbcjr_hip.so).
+"""Loaders of the engine's two libraries.
 
-This is the binding a maintainer would add on the reference side: it passes raw
-device pointers, sizes and the current HIP stream.  torch supplies device memory
-and streams only.  There is no fallback: if the library is missing or fails to
-load, every entry point raises.
+libbcjr_torch.so registers the `bcjr` torch operators in C++ (TORCH_LIBRARY,
+csrc/bcjr_torch.cpp) over the C ABI of libbcjr_hip.so; the package calls the
+engine only through those operators (torch.ops.bcjr.*).  load() is the ctypes
+binding of the raw C ABI in include/bcjr_hip.h -- the binding a maintainer
+would add on a reference side without torch: raw device pointers, sizes and a
+HIP stream -- used by the ABI tests.  There is no fallback: if a library is
+missing or fails to load, every entry point raises.
 """
 from __future__ import annotations
 
 import ctypes
 import os
+import re
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libbcjr_hip.so")
+OPS_PATH = os.path.join(_HERE, "libbcjr_torch.so")
 
 CODE_TABLE, CODE_1MAD, CODE_3INST, CODE_HYB = 0, 1, 2, 3
 OP_FORWARD, OP_BACKWARD, OP_VITERBI = 0, 1, 2
@@ -38,6 +43,44 @@ class BcjrError(RuntimeError):
     def __init__(self, status: int, what: str, detail: str):
         super().__init__(f"{what} failed: {detail or 'status %d' % status}")
         self.status = status
+
+
+_ops_loaded = False
+
+
+def load_ops():
+    """torch.ops.bcjr, after loading libbcjr_torch.so (once).  It links
+    libbcjr_hip.so from its own directory."""
+    global _ops_loaded
+    import torch
+    if not _ops_loaded:
+        if not os.path.exists(OPS_PATH):
+            raise RuntimeError(
+                f"BCJR torch operator library not found at {OPS_PATH}; build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'` (or make -C quant-2bit_amd/csrc)")
+        torch.ops.load_library(OPS_PATH)
+        _ops_loaded = True
+    return torch.ops.bcjr
+
+
+# A failed C ABI call inside an operator raises RuntimeError("bcjr status <n>:
+# <entry point> failed: <detail>"); run_op re-raises it as BcjrError.
+_STATUS = re.compile(r"bcjr status (-?\d+): (\w+) failed: ([^\n]*)")
+
+
+def run_op(op, *args):
+    """op(*args), with a failed C ABI call re-raised as BcjrError (under
+    torch.compile the operator is traced as it is)."""
+    import torch
+    if torch.compiler.is_compiling():
+        return op(*args)
+    try:
+        return op(*args)
+    except RuntimeError as e:
+        m = _STATUS.search(str(e))
+        if m is None:
+            raise
+        raise BcjrError(int(m.group(1)), m.group(2), m.group(3)) from None
 
 
 _lib = None

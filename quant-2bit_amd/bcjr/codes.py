@@ -151,7 +151,15 @@ def resolve_codebook(codebook: torch.Tensor, L: int, k: int, V: int, device: tor
 
     Raises AssertionError when the codebook's shape is not (2^L, V) or it lives
     on another device than the sequences (the reference fails there too: a
-    device mismatch in its einsum, src/bcjr/forward_backward.py:100)."""
+    device mismatch in its einsum, src/bcjr/forward_backward.py:100).
+
+    The recognition of an untagged table is cached per storage and re-run when
+    the tensor's version counter moves (any in-place torch op on it).  Writes
+    that bypass the counter -- through `.data`, or by another kernel or library
+    writing through `data_ptr()` -- leave the cached result in place, and a
+    table recognised as 1MAD/3INST/HYB would keep running on the hashed / LUT
+    kernels with its old contents.  Call forget(codebook) after such a write
+    (the reference reads the table on every call and has no such cache)."""
     if tuple(codebook.shape) != (1 << L, V):
         raise AssertionError(f"codebook must be ({1 << L}, {V}); got {tuple(codebook.shape)}")
     device = _canonical(device)
@@ -201,4 +209,13 @@ def resolve_codebook(codebook: torch.Tensor, L: int, k: int, V: int, device: tor
     return Spec(L, k, V, code), None
 
 
-__all__ = ["make_1mad_codebook", "make_3inst_codebook", "make_hyb_codebook_gpu", "code_of", "resolve_codebook"]
+def forget(codebook: torch.Tensor) -> None:
+    """Drop the recognition result cached for codebook's storage, so the next
+    resolve_codebook examines its contents afresh.  Needed only after a write
+    that bypasses the tensor's version counter (see resolve_codebook); a
+    generator tag (make_*_codebook) is not affected."""
+    _SEEN.pop(id(codebook.untyped_storage()), None)
+
+
+__all__ = ["make_1mad_codebook", "make_3inst_codebook", "make_hyb_codebook_gpu", "code_of", "resolve_codebook",
+           "forget"]

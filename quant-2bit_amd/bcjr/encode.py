@@ -20,6 +20,9 @@ one more launch (bcjr_viterbi_trace) with the same rounding and tie rules.
 """
 from __future__ import annotations
 
+import hashlib
+from collections import OrderedDict
+
 import numpy as np
 import torch
 
@@ -64,8 +67,29 @@ def _device():
     return torch.device("cuda", torch.cuda.current_device())
 
 
+# Device codebooks of the numpy-facing calls, keyed by their contents: each call
+# evaluates decode_fn (as the reference does, encode.py:233-247) and reuses the
+# device tensor of an identical table, so its recognition (resolve_codebook) is
+# cached across calls instead of re-run on a new tensor every time.  Keyed by
+# content, not by decode_fn, a decode_fn whose table changes (a LUT updated in
+# place) gets a fresh tensor.  A few tables at most are kept.
+_GPU_TABLES: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+_GPU_TABLES_MAX = 8
+
+
 def _gpu_codebook(L, V, decode_fn):
-    return torch.from_numpy(precompute_codebook_v(L, V, decode_fn)).to(_device())
+    table = precompute_codebook_v(L, V, decode_fn)
+    dev = _device()
+    key = (L, V, str(dev), hashlib.blake2b(table.tobytes(), digest_size=16).digest())
+    cb = _GPU_TABLES.get(key)
+    if cb is None:
+        cb = torch.from_numpy(table).to(dev)
+        _GPU_TABLES[key] = cb
+        while len(_GPU_TABLES) > _GPU_TABLES_MAX:
+            _GPU_TABLES.popitem(last=False)
+    else:
+        _GPU_TABLES.move_to_end(key)
+    return cb
 
 
 def _sequences(sequences, V):

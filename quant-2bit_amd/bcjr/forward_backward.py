@@ -7,11 +7,13 @@ return values and assertion behaviour.  The whole forward (alpha and beta
 recursions, marginals, soft codeword, log Z) is one kernel launch, and the
 backward is one more; autograd saves only the inputs.
 
-The node is a pair of registered torch operators, bcjr::forward and
-bcjr::backward (torch.library.custom_op), with fake (meta) implementations and
-an autograd formula, so torch.compile traces through it without a graph break
+The node is the registered torch operator bcjr::node (torch.library.custom_op,
+with a fake implementation and an autograd formula whose backward is
+bcjr::node_backward), so torch.compile traces through it without a graph break
 (the reference compiles its node: src/bcjr/forward_backward_fast.py:33-44,
-src/tripwires/test_bcjr_compile.py:28-84).
+src/tripwires/test_bcjr_compile.py:28-84).  Inside, it resolves the codebook
+and calls the C++ operators bcjr::forward / bcjr::backward (libbcjr_torch.so,
+TORCH_LIBRARY over the C ABI).
 
 Trellis (forward_backward.py:1-45): S = 2^L states, kV = k*V bits per step,
 next = ((s << kV) | c) & (S-1); emission ll_t(s) = -||c(s) - w_t||^2 / T;
@@ -94,10 +96,11 @@ def _check_T(T: Tensor, B: int):
 # Registered operators
 # ---------------------------------------------------------------------------
 
-@torch.library.custom_op("bcjr::forward", mutates_args=())
+@torch.library.custom_op("bcjr::node", mutates_args=())
 def bcjr_forward_op(sequences: Tensor, codebook: Tensor, T: Tensor, L: int, k: int,
                     V: int) -> tuple[Tensor, Tensor]:
-    """soft (B, N, V) and log Z (B,), float32 (bcjr_forward)."""
+    """soft (B, N, V) and log Z (B,), float32: the node's forward on a (2^L, V)
+    codebook (resolved here, then bcjr::forward)."""
     _check_T(T, sequences.shape[0])
     spec, table = resolve_codebook(codebook, L, k, V, sequences.device)
     return ops.forward(spec, sequences, T, table)
@@ -110,11 +113,11 @@ def _(sequences, codebook, T, L, k, V):
             sequences.new_empty((B,), dtype=torch.float32))
 
 
-@torch.library.custom_op("bcjr::backward", mutates_args=())
+@torch.library.custom_op("bcjr::node_backward", mutates_args=())
 def bcjr_backward_op(sequences: Tensor, codebook: Tensor, T: Tensor, g_soft: Tensor,
                      g_logZ: Optional[Tensor], L: int, k: int, V: int) -> Tensor:
     """d sequences (B, N, V) float32 of sum(g_soft * soft) + sum(g_logZ * logZ)
-    (bcjr_backward)."""
+    (the codebook resolved, then bcjr::backward)."""
     _check_T(T, sequences.shape[0])
     spec, table = resolve_codebook(codebook, L, k, V, sequences.device)
     return ops.backward(spec, sequences, T, table, g_soft, g_logZ)
@@ -169,8 +172,8 @@ class BcjrInternalsFunction(torch.autograd.Function):
 
 
 class BcjrFunction:
-    """The node as one autograd function (forward = bcjr::forward, backward =
-    bcjr::backward): BcjrFunction.apply(sequences, codebook, T, L, k, V)."""
+    """The node as one autograd function (forward = bcjr::node, backward =
+    bcjr::node_backward): BcjrFunction.apply(sequences, codebook, T, L, k, V)."""
 
     @staticmethod
     def apply(sequences, codebook, T, L, k, V):

@@ -15,8 +15,6 @@ the inverse transform, so the autograd backward of each is the other one.
 """
 from __future__ import annotations
 
-import ctypes
-
 import numpy as np
 import torch
 
@@ -30,32 +28,10 @@ def make_sign_vector(n, seed):
     return rng.choice([-1.0, 1.0], size=n).astype(np.float32)
 
 
-def _stream(device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
-
-
-def _hadamard(x: torch.Tensor, scale: float) -> torch.Tensor:
-    if not x.is_cuda or x.dtype != torch.float32:
-        raise AssertionError("hadamard_transform expects a float32 GPU tensor")
-    n = x.shape[-1]
-    xc = x.contiguous()
-    out = torch.empty_like(xc)
-    rows = xc.numel() // n if n else 0
-    with torch.cuda.device(x.device):
-        _lib.check(_lib.load().bcjr_hadamard(_lib.ptr(xc), _lib.ptr(out), rows, n, float(scale),
-                                             _stream(x.device)), "bcjr_hadamard")
-    return out
-
-
-@torch.library.custom_op("bcjr::hadamard", mutates_args=())
-def hadamard_op(x: torch.Tensor, scale: float) -> torch.Tensor:
-    """scale * H_n x along the last axis (bcjr_hadamard)."""
-    return _hadamard(x, scale)
-
-
-@hadamard_op.register_fake
-def _(x, scale):
-    return torch.empty(x.shape, dtype=torch.float32, device=x.device)
+# The transforms are the C++ operators bcjr::hadamard, bcjr::rht and
+# bcjr::rht_batched (csrc/bcjr_torch.cpp, with their Meta kernels); their
+# autograd formulas are registered here.
+_ops = _lib.load_ops()
 
 
 def _hadamard_setup(ctx, inputs, output):
@@ -63,17 +39,39 @@ def _hadamard_setup(ctx, inputs, output):
 
 
 def _hadamard_backward(ctx, g):  # H is symmetric
-    return hadamard_op(g.contiguous(), ctx.scale), None
+    return _ops.hadamard(g.contiguous(), ctx.scale), None
 
 
-hadamard_op.register_autograd(_hadamard_backward, setup_context=_hadamard_setup)
+torch.library.register_autograd("bcjr::hadamard", _hadamard_backward, setup_context=_hadamard_setup)
+
+
+def _rht_setup(ctx, inputs, output):
+    W, sign_l, sign_r, inverse = inputs
+    ctx.save_for_backward(sign_l, sign_r)
+    ctx.inverse = inverse
+
+
+def _rht_backward(ctx, g):  # the adjoint of the transform is its inverse
+    sign_l, sign_r = ctx.saved_tensors
+    return _ops.rht(g.contiguous(), sign_l, sign_r, not ctx.inverse), None, None, None
+
+
+def _rht_batched_backward(ctx, g):
+    sign_l, sign_r = ctx.saved_tensors
+    return _ops.rht_batched(g.contiguous(), sign_l, sign_r, not ctx.inverse), None, None, None
+
+
+torch.library.register_autograd("bcjr::rht", _rht_backward, setup_context=_rht_setup)
+torch.library.register_autograd("bcjr::rht_batched", _rht_batched_backward, setup_context=_rht_setup)
 
 
 def hadamard_transform(x: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
     """scale * H_n x along the last axis (unscaled Sylvester H_n, n a power of two): the
     fast_hadamard_transform call of src/qat/ste.py:113-135, with the butterflies of
     src/rht/transform.py:26-42 (fwht_numpy)."""
-    return hadamard_op(x, float(scale))
+    if not x.is_cuda or x.dtype != torch.float32:
+        raise AssertionError("hadamard_transform expects a float32 GPU tensor")
+    return _lib.run_op(_ops.hadamard, x, float(scale))
 
 
 def _check_rht_args(W, sign_l, sign_r):
@@ -85,80 +83,30 @@ def _check_rht_args(W, sign_l, sign_r):
                              f"{tuple(sign_r.shape)}")
 
 
-def _rht(W, sign_l, sign_r, inverse: bool) -> torch.Tensor:
-    _check_rht_args(W, sign_l, sign_r)
-    m, n = W.shape
-    Wc = W.detach().contiguous()
-    sl = sign_l.detach().to(device=W.device, dtype=torch.float32).contiguous()
-    sr = sign_r.detach().to(device=W.device, dtype=torch.float32).contiguous()
-    out = torch.empty_like(Wc)
-    with torch.cuda.device(W.device):
-        _lib.check(_lib.load().bcjr_rht(_lib.ptr(Wc), _lib.ptr(out), m, n, _lib.ptr(sl), _lib.ptr(sr),
-                                        1 if inverse else 0, _stream(W.device)), "bcjr_rht")
-    return out
-
-
-@torch.library.custom_op("bcjr::rht", mutates_args=())
-def rht_op(W: torch.Tensor, sign_l: torch.Tensor, sign_r: torch.Tensor, inverse: bool) -> torch.Tensor:
-    """The RHT of W (m, n), or its inverse (bcjr_rht)."""
-    return _rht(W, sign_l, sign_r, inverse)
-
-
-@rht_op.register_fake
-def _(W, sign_l, sign_r, inverse):
-    if W.dim() != 2 or tuple(sign_l.shape) != (W.shape[0],) or tuple(sign_r.shape) != (W.shape[1],):
-        raise AssertionError(f"RHT of {tuple(W.shape)} with signs {tuple(sign_l.shape)}, {tuple(sign_r.shape)}")
-    return torch.empty(W.shape, dtype=torch.float32, device=W.device)
-
-
-def _rht_setup(ctx, inputs, output):
-    W, sign_l, sign_r, inverse = inputs
-    ctx.save_for_backward(sign_l, sign_r)
-    ctx.inverse = inverse
-
-
-def _rht_backward(ctx, g):  # the adjoint of the transform is its inverse
-    sign_l, sign_r = ctx.saved_tensors
-    return rht_op(g.contiguous(), sign_l, sign_r, not ctx.inverse), None, None, None
-
-
-rht_op.register_autograd(_rht_backward, setup_context=_rht_setup)
-
-
-def _rht_batched(W, sign_l, sign_r, inverse: bool) -> torch.Tensor:
+def _check_rht_batched_args(W, sign_l, sign_r):
     if W.dim() != 3 or not W.is_cuda or W.dtype != torch.float32:
         raise AssertionError(f"W must be a 3-D float32 GPU tensor; got {tuple(W.shape)} {W.dtype}")
     E, m, n = W.shape
     if tuple(sign_l.shape) != (E, m) or tuple(sign_r.shape) != (E, n):
         raise AssertionError(f"sign vectors must be ({E}, {m}) and ({E}, {n}); got {tuple(sign_l.shape)}, "
                              f"{tuple(sign_r.shape)}")
-    Wc = W.detach().contiguous()
-    sl = sign_l.detach().to(device=W.device, dtype=torch.float32).contiguous()
-    sr = sign_r.detach().to(device=W.device, dtype=torch.float32).contiguous()
-    out = torch.empty_like(Wc)
-    with torch.cuda.device(W.device):
-        _lib.check(_lib.load().bcjr_rht_batched(_lib.ptr(Wc), _lib.ptr(out), E, m, n, _lib.ptr(sl), _lib.ptr(sr),
-                                                1 if inverse else 0, _stream(W.device)), "bcjr_rht_batched")
-    return out
 
 
-@torch.library.custom_op("bcjr::rht_batched", mutates_args=())
-def rht_batched_op(W: torch.Tensor, sign_l: torch.Tensor, sign_r: torch.Tensor, inverse: bool) -> torch.Tensor:
-    """The RHT (or its inverse) of each matrix of W (E, m, n) (bcjr_rht_batched)."""
-    return _rht_batched(W, sign_l, sign_r, inverse)
+def _signs(v, like):
+    return v.to(device=like.device, dtype=torch.float32)
 
 
-@rht_batched_op.register_fake
-def _(W, sign_l, sign_r, inverse):
-    return torch.empty(W.shape, dtype=torch.float32, device=W.device)
+def rht_op(W, sign_l, sign_r, inverse: bool) -> torch.Tensor:
+    """The RHT of W (m, n), or its inverse (bcjr::rht over bcjr_rht)."""
+    _check_rht_args(W, sign_l, sign_r)
+    return _lib.run_op(_ops.rht, W, _signs(sign_l, W), _signs(sign_r, W), bool(inverse))
 
 
-def _rht_batched_backward(ctx, g):
-    sign_l, sign_r = ctx.saved_tensors
-    return rht_batched_op(g.contiguous(), sign_l, sign_r, not ctx.inverse), None, None, None
-
-
-rht_batched_op.register_autograd(_rht_batched_backward, setup_context=_rht_setup)
+def rht_batched_op(W, sign_l, sign_r, inverse: bool) -> torch.Tensor:
+    """The RHT (or its inverse) of each matrix of W (E, m, n) (bcjr::rht_batched
+    over bcjr_rht_batched)."""
+    _check_rht_batched_args(W, sign_l, sign_r)
+    return _lib.run_op(_ops.rht_batched, W, _signs(sign_l, W), _signs(sign_r, W), bool(inverse))
 
 
 def apply_rht_batched(W, sign_l, sign_r):

@@ -536,7 +536,11 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
             for (int v = 0; v < V; ++v) ga[v] = c ? fmaf(wgt, hh[c][v], ga[v]) : wgt * hh[c][v];
           }
-          const float G = fexp2(pms + M);
+          // (pms + 0 does not fold: -0 + 0 is +0)
+          const float G = SHIFT ? fexp2(pms + M) : fexp2(pms);
+          // sum_s dll_t(s) is g_Z in exact arithmetic, but its computed value
+          // cancels the common-mode rounding of (phi + psi - E[F]) in
+          // A1 - w A0, which grows with N: it is accumulated, not assumed.
           a0 = G * fmaf(Dp, s, ez);
 #pragma unroll
           for (int v = 0; v < V; ++v) a1[v] = G * ga[v];
@@ -600,15 +604,13 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
             if constexpr (kPair) {
               float no[R], nuo[R], smin = 0.0f, ua0 = 0.0f, ua1[V];
 #pragma unroll
-              for (int v = 0; v < V; ++v) ua1[v] = 0.0f;
-#pragma unroll
               for (int p = 0; p < R; ++p) {
                 float a0, a1[V];
                 const float s = beta_out(Fast{}, i, p, xu, u, nr, nui, pm[p] + kts, pmu[p], oout, no[p], nuo[p], a0, a1);
                 smin = p ? fminf(smin, s) : s;
-                ua0 += a0;
+                ua0 = p ? ua0 + a0 : a0;
 #pragma unroll
-                for (int v = 0; v < V; ++v) ua1[v] += a1[v];
+                for (int v = 0; v < V; ++v) ua1[v] = p ? ua1[v] + a1[v] : a1[v];
               }
               if constexpr (!EXACT) {
                 if (smin < kUnderflow) {
@@ -639,16 +641,14 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
               const float* src = slot_src(t, i);
               float smin = 0.0f, ua0 = 0.0f, ua1[V];
 #pragma unroll
-              for (int v = 0; v < V; ++v) ua1[v] = 0.0f;
-#pragma unroll
               for (int p = 0; p < R; ++p) {
                 float no, nuo, a0, a1[V];
                 const float pms = src[2 * p] + kts, pmup = src[2 * p + 1];
                 const float s = beta_out(Fast{}, i, p, xu, u, nr, nui, pms, pmup, oout, no, nuo, a0, a1);
                 smin = p ? fminf(smin, s) : s;
-                ua0 += a0;
+                ua0 = p ? ua0 + a0 : a0;
 #pragma unroll
-                for (int v = 0; v < V; ++v) ua1[v] += a1[v];
+                for (int v = 0; v < V; ++v) ua1[v] = p ? ua1[v] + a1[v] : a1[v];
                 lds_pair(yi ^ koff(p)) = make_float2(no, nuo);
                 tmax = fmaxf(tmax, no);
               }
@@ -721,7 +721,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #define BCJR_BWD_CASE(KV_, V_, CODE_, UPT_)                                                  \
   if (KV == KV_ && V == V_ && code == CODE_ && upt == UPT_)                                 \
     return reinterpret_cast<const void*>(                                                   \
-        &bcjr_bwd_kernel<KV_, V_, CODE_, UPT_, bwd_cached_units(KV_, V_, UPT_),          \
+        &bcjr_bwd_kernel<KV_, V_, CODE_, UPT_, bwd_cached_units(KV_, V_, UPT_, CODE_),   \
                          bwd_alpha_cached_units(KV_, V_, UPT_)>);
 
 #define BCJR_BWD_UPTS(KV_, V_, CODE_) \

@@ -316,9 +316,12 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
                                         !pl->cache && pl->nthr == 1024);
     if (op == OP_FWD && KV == 2 && p->V == 1 && p->L >= 14 && p->code <= BCJR_CODE_3INST) {
       // Four waves per SIMD: 1024 threads, every codeword in VGPRs (bcjr_fwd4.hip).
+      // Kept only where its larger LDS (N doubles and floats beside the state)
+      // still fits; otherwise the 512-thread plan stands (at L = 16 it holds
+      // N = 2704, the 1024-thread kernel N = 2702).
       const int upt4 = 1 << (p->L - 14);
       const void* fn4 = bcjr::fwd4_kernel_ptr(p->code, upt4);
-      if (fn4) {
+      if (fn4 && bcjr::fwd4_lds_bytes(p->L, N) <= di.max_lds) {
         pl->fn = fn4;
         pl->nthr = nthr = 1024;
         pl->upt = upt4;
@@ -680,11 +683,16 @@ int bcjr_viterbi_trace(const bcjr_problem* prob, const float* seq, const float* 
   const int NT = 1 << (prob->L - KV);
   const int nthr = NT < 64 ? 64 : (NT > 1024 ? 1024 : NT);
   const size_t lds = (size_t)NT * (sizeof(float) + 1);
+  if (lds > di.max_lds)
+    return fail(BCJR_EUNSUPPORTED, "viterbi trace needs %zu bytes of LDS per workgroup (device limit %zu)", lds,
+                di.max_lds);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
   const long long cap = (long long)di.num_cu * 2;
   const unsigned grid = (unsigned)(prob->B < cap ? prob->B : cap);
   bcjr::TraceParams P = {seq, codebook_or_lut, trace, backptr, prob->B, (int)prob->N, prob->L, prob->Q};
   void* args[] = {&P};
-  hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(nthr), args, lds, stream);
+  e = hipLaunchKernel(fn, dim3(grid), dim3(nthr), args, lds, stream);
   if (e != hipSuccess) return hip_fail(e, "hipLaunchKernel(viterbi_trace)");
   return BCJR_OK;
 }

@@ -253,11 +253,13 @@ __device__ __forceinline__ void raw_codeword(uint32_t xu, uint32_t off, uint32_t
 // Group log-sum-exp.  The R inputs of a butterfly are normalised by their
 // maximum, so every term 2^a of a group is <= 1 and, at moderate temperature,
 // the group sum needs no per-group maximum: one exp2 per term, no compare or
-// subtract.  A butterfly with a group sum below kUnderflow (every term of the
-// group < -120) is recomputed against the group maxima (exec-masked, rare for
-// T >= kExactBelowT).  Below kExactBelowT that fallback would fire in most
-// waves, so sequences with a lower temperature use the group maxima throughout.
-constexpr float kUnderflow = 0x1p-120f;
+// subtract.  v_exp_f32 flushes results below 2^-126 to zero, so a group whose
+// sum is s loses at most (R - 1) 2^-126 / s of it; a butterfly with a group sum
+// below kUnderflow = 2^-100 (loss then under 2^-22 relative) is recomputed
+// against the group maxima (exec-masked, rare for T >= kExactBelowT).  Below
+// kExactBelowT that fallback would fire in most waves, so sequences with a
+// lower temperature use the group maxima throughout.
+constexpr float kUnderflow = 0x1p-100f;
 constexpr float kExactBelowT = 0.08f;
 // The 1024-thread forward's switch point.  Its exact variant hashes every
 // codeword (the cache does not fit beside that variant's working set in 128

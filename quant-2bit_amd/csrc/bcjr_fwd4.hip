@@ -338,7 +338,8 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
                 ec = c ? fmaf(e, hv(i, p, c), ec) : e * hv(i, p, c);
               }
               sp[p] = s;
-              ua = fmaf(fexp2(pm[p] + kts), ec, ua);
+              const float G = fexp2(pm[p] + kts);
+              ua = p ? fmaf(G, ec, ua) : G * ec;
               no[p] = flog2(s) + off;
             }
             const float smin = fminf(fminf(sp[0], sp[1]), fminf(sp[2], sp[3]));

@@ -24,13 +24,17 @@ constexpr int fwd_cached_units(int KV, int V, int upt) {
 }
 
 // The same budget for the backward's beta + nu + grad sweep: 5 of 8
-// butterflies at kV = 2, V = 1 (80 VGPRs beside that sweep's working set;
-// a sixth fits but measured the same), 2 at V = 2.
+// butterflies at kV = 2, V = 1 (80 VGPRs beside that sweep's working set), 2 at
+// V = 2.  The 3INST instance, whose hashed codewords need no table address,
+// keeps a sixth (96 VGPRs; a seventh or eighth spills inside the step loop and
+// runs 5 % slower); the table and 1MAD instances spill at 96.
 constexpr int kBwdCacheVgprs = 80;
-constexpr int bwd_cached_units(int KV, int V, int upt) {
+constexpr int kBwdCacheVgprs3Inst = 96;
+constexpr int bwd_cached_units(int KV, int V, int upt, int code = -1) {
   return KV >= 4 ? 0
-                 : (upt < kBwdCacheVgprs / ((1 << KV) * (1 << KV) * V) ? upt
-                                                                        : kBwdCacheVgprs / ((1 << KV) * (1 << KV) * V));
+                 : (upt < (code == 2 ? kBwdCacheVgprs3Inst : kBwdCacheVgprs) / ((1 << KV) * (1 << KV) * V)
+                        ? upt
+                        : (code == 2 ? kBwdCacheVgprs3Inst : kBwdCacheVgprs) / ((1 << KV) * (1 << KV) * V));
 }
 
 // The alpha + mu sweep's own budget (its working set is smaller than the beta

@@ -370,18 +370,36 @@ def test_one_bit_per_step_takes_the_table_kernels():
 
 
 def test_registered_ops_have_fake_implementations():
-    """bcjr::forward / bcjr::backward / bcjr::rht are torch operators whose
-    fake (meta) implementations give the output shapes without a device."""
+    """The engine's torch operators are registered in C++ (libbcjr_torch.so,
+    TORCH_LIBRARY) with Meta kernels, and the node (bcjr::node, bcjr::node_backward)
+    in Python over them: fake tensors give every output shape without a device."""
     from torch._subclasses.fake_tensor import FakeTensorMode
-    import bcjr  # noqa: F401  (registers the operators)
+    import bcjr  # noqa: F401  (loads the operator library, registers the node)
+    from bcjr import _lib
+    assert _lib._ops_loaded and os.path.exists(_lib.OPS_PATH)
+    for name in ("forward", "forward_internals", "forward_entropy", "backward", "viterbi", "decode", "viterbi_trace",
+                 "dequant", "codebook", "hadamard", "rht", "rht_batched"):
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(f"bcjr::{name}", "CUDA"), name
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(f"bcjr::{name}", "Meta"), name
     with FakeTensorMode():
         seq = torch.empty(5, 32, 1)
         cb = torch.empty(1 << 8, 1)
         T = torch.empty(1)
-        soft, logZ = torch.ops.bcjr.forward(seq, cb, T, 8, 2, 1)
+        soft, logZ = torch.ops.bcjr.node(seq, cb, T, 8, 2, 1)
         assert soft.shape == (5, 32, 1) and logZ.shape == (5,) and soft.dtype == torch.float32
-        d = torch.ops.bcjr.backward(seq, cb, T, torch.empty(5, 32, 1), None, 8, 2, 1)
+        d = torch.ops.bcjr.node_backward(seq, cb, T, torch.empty(5, 32, 1), None, 8, 2, 1)
         assert d.shape == (5, 32, 1)
+        soft, logZ = torch.ops.bcjr.forward(seq, T, None, 8, 2, 1, _lib.CODE_3INST, 9)
+        assert soft.shape == (5, 32, 1) and logZ.shape == (5,)
+        assert torch.ops.bcjr.backward(seq, T, None, seq, None, 8, 2, 1, _lib.CODE_3INST, 9).shape == (5, 32, 1)
+        outs = torch.ops.bcjr.forward_internals(seq, T, cb, 8, 2, 1, _lib.CODE_TABLE, 9)
+        assert [tuple(o.shape) for o in outs] == [(5, 32, 1), (5,), (5, 32, 256), (5, 32, 256), (5, 32, 256)]
+        walk, bits, start, recon, mse, packed = torch.ops.bcjr.viterbi(seq, None, 8, 2, 1, _lib.CODE_3INST, 9, True)
+        assert walk.shape == bits.shape == (5, 32) and start.shape == (5,) and recon.shape == (5, 32, 1)
+        assert packed.shape == (5, 8) and packed.dtype == torch.uint8 and walk.dtype == torch.int32
+        assert torch.ops.bcjr.dequant(torch.empty(4, dtype=torch.int32), None, None, torch.empty(4, 64, dtype=torch.uint8),
+                                      32, 32, 16, 16, 1.0, 8, 2, 1, _lib.CODE_3INST, 9).shape == (32, 32)
+        assert torch.ops.bcjr.codebook(torch.empty(0), None, 8, _lib.CODE_1MAD, 9).shape == (256, 1)
         W = torch.empty(64, 32)
         out = torch.ops.bcjr.rht(W, torch.empty(64), torch.empty(32), False)
         assert out.shape == (64, 32)

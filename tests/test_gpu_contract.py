@@ -218,3 +218,45 @@ def test_torch_compile_fullgraph_quantize_weight(bcjr_mod):
         outs.append((Wq.detach(), W.grad))
     assert max_rel(outs[1][0].cpu().numpy(), outs[0][0].cpu().numpy()) < 1e-6
     assert max_rel(outs[1][1].cpu().numpy(), outs[0][1].cpu().numpy()) < 1e-6
+
+
+def test_forget_after_writes_that_bypass_the_version_counter(bcjr_mod):
+    """A table recognised as 3INST and then changed through .data (no version
+    bump) keeps its cached recognition until forget(); afterwards it is examined
+    afresh and runs on the table kernels."""
+    _say("forget")
+    from bcjr import ops
+    from bcjr.codes import forget, resolve_codebook
+    dev = torch.device("cuda")
+    L = 12
+    plain = bcjr_mod.make_3inst_codebook(L, dev).clone()
+    assert resolve_codebook(plain, L, 2, 1, dev)[0].code == ops.CODE_3INST
+    plain.data[7, 0] += 1.0  # bypasses the version counter
+    assert resolve_codebook(plain, L, 2, 1, dev)[0].code == ops.CODE_3INST  # stale by design
+    forget(plain)
+    spec, table = resolve_codebook(plain, L, 2, 1, dev)
+    assert spec.code == ops.CODE_TABLE and table.data_ptr() == plain.data_ptr()
+
+
+def test_numpy_api_reuses_device_tables_by_content(bcjr_mod):
+    """viterbi_encode_v builds its device table from decode_fn on each call; an
+    identical table reuses one device tensor (its recognition cached), and a
+    decode_fn whose table changed in place gets a fresh one."""
+    _say("numpy-api table cache")
+    from bcjr import encode
+    L, V = 10, 2
+    lut = np.random.default_rng(4).standard_normal((1 << L, V)).astype(np.float32)
+
+    def decode(states):
+        return lut[states]
+
+    a = encode._gpu_codebook(L, V, decode)
+    b = encode._gpu_codebook(L, V, decode)
+    assert a is b
+    lut[3] += 1.0
+    c = encode._gpu_codebook(L, V, decode)
+    assert c is not a and np.array_equal(c.cpu().numpy(), lut)
+    seq = np.random.default_rng(5).standard_normal(64).astype(np.float32)
+    r1 = bcjr_mod.viterbi_encode_v(seq, L, 1, V, decode)
+    r2 = bcjr_mod.viterbi_encode_v(seq, L, 1, V, decode)
+    assert np.array_equal(r1[0], r2[0]) and r1[1] == r2[1]
