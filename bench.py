@@ -609,7 +609,7 @@ def main():
     soft_s = fwd_s + bwd_s
     per_cell = trans_per_cell_grad(2)
     traffic = read_traffic()
-    roofline = {"bound": "valu_exp", "kernel": "bcjr_fwd4_kernel<2,4> + bcjr_bwd_kernel<2,1,2,8,5,8> (the layer's soft launches)",
+    roofline = {"bound": "valu_exp", "kernel": "bcjr_fwd4_kernel<2,4> + bcjr_bwd_kernel<2,1,2,8,6,8> (the layer's soft launches)",
                 "achieved": per_cell * cells / soft_s / 1e12, "peak": exp_peak / 1e12, "unit": "Texp/s",
                 "frac": per_cell * cells / soft_s / exp_peak, "traffic": traffic,
                 "per_cell": per_cell, "cells": cells, "launch_s": soft_s,
