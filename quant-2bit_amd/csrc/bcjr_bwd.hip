@@ -281,9 +281,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           }
           float M = 0.0f;
           if constexpr (SHIFT) {
-            M = a[0];
-#pragma unroll
-            for (int p = 1; p < R; ++p) M = fmaxf(M, a[p]);
+            M = max_of_inputs(a);
           }
           float e = fexp2(a[0] - M);
           float s = e, ephi = e * phi[0];
@@ -352,8 +350,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
               for (int r = 0; r < R; ++r) {
                 lds_pair(yi ^ koff(r)) = make_float2(mo[r], muo[r]);
-                tmax = fmaxf(tmax, mo[r]);
               }
+              tmax = max_with(tmax, mo);
             } else if constexpr (kColUnroll) {
               // Outputs unrolled, so every state's LUT offset is an immediate; a
               // butterfly with an underflowed group is redone output by output
@@ -365,7 +363,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
                 const float s = alpha_out(Fast{}, i, r, xu, u, m, mui, oout, mo, muo, cbs[r]);
                 smin = r ? fminf(smin, s) : s;
                 lds_pair(yi ^ koff(r)) = make_float2(mo, muo);
-                tmax = fmaxf(tmax, mo);
+                tmax = vmax_raw(tmax, mo);
               }
               if constexpr (!EXACT) {
                 if (smin < kUnderflow) {
@@ -375,7 +373,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
                     alpha_out(std::true_type{}, i, r, xu, u, m, mui, oout, mo, muo,
                               hyb_col_base((uint32_t)(R * u + r), P.Q));
                     lds_pair(yi ^ koff(r)) = make_float2(mo, muo);
-                    tmax = fmaxf(tmax, mo);
+                    tmax = vmax_raw(tmax, mo);
                   }
                 }
               }
@@ -387,7 +385,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
                 const float s = alpha_out(Fast{}, i, r, xu, u, m, mui, oout, mo, muo, cb);
                 if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, i, r, xu, u, m, mui, oout, mo, muo, cb);
                 lds_pair(yi ^ koff(r)) = make_float2(mo, muo);
-                tmax = fmaxf(tmax, mo);
+                tmax = vmax_raw(tmax, mo);
               }
             }
           }
@@ -518,9 +516,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           }
           float M = 0.0f;
           if constexpr (SHIFT) {
-            M = y[0];
-#pragma unroll
-            for (int c = 1; c < R; ++c) M = fmaxf(M, y[c]);
+            M = max_of_inputs(y);
           }
           const float Dp = pmu - EFg;  // mu_{t-1} - E[F] + g_Z
           float s = 0.0f, ez = 0.0f, ga[V];
@@ -633,8 +629,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
               for (int p = 0; p < R; ++p) {
                 lds_pair(yi ^ koff(p)) = make_float2(no[p], nuo[p]);
-                tmax = fmaxf(tmax, no[p]);
               }
+              tmax = max_with(tmax, no);
             } else if constexpr (kColUnroll) {
               // Outputs unrolled (immediate LUT offsets); the butterfly's gradient
               // sums are redone when a group underflowed.
@@ -650,7 +646,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
                 for (int v = 0; v < V; ++v) ua1[v] = p ? ua1[v] + a1[v] : a1[v];
                 lds_pair(yi ^ koff(p)) = make_float2(no, nuo);
-                tmax = fmaxf(tmax, no);
+                tmax = vmax_raw(tmax, no);
               }
               if constexpr (!EXACT) {
                 if (smin < kUnderflow) {
@@ -666,7 +662,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
                     for (int v = 0; v < V; ++v) ua1[v] += a1[v];
                     lds_pair(yi ^ koff(p)) = make_float2(no, nuo);
-                    tmax = fmaxf(tmax, no);
+                    tmax = vmax_raw(tmax, no);
                   }
                 }
               }
@@ -686,7 +682,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
                 for (int v = 0; v < V; ++v) A1[v] += a1[v];
                 lds_pair(yi ^ koff(p)) = make_float2(no, nuo);
-                tmax = fmaxf(tmax, no);
+                tmax = vmax_raw(tmax, no);
               }
             }
           }

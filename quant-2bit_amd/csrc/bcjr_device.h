@@ -23,6 +23,7 @@
 
 #include <type_traits>
 #include <stdint.h>
+#include <climits>
 
 namespace bcjr {
 
@@ -320,6 +321,16 @@ __device__ __forceinline__ float vmax_raw(float a, float b) {
   asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
+// max(m, v[0], ..., v[n-1]) in v_max3_f32 steps, on the raw operands like
+// max_of_inputs (none is NaN): the running maximum of a step's outputs.
+template <int n>
+__device__ __forceinline__ float max_with(float m, const float (&v)[n]) {
+  int i = 0;
+#pragma unroll
+  for (; i + 1 < n; i += 2) m = vmax3_raw(m, v[i], v[i + 1]);
+  if (i < n) m = vmax_raw(m, v[i]);
+  return m;
+}
 template <int n>
 __device__ __forceinline__ float max_of_inputs(const float (&v)[n]) {
   static_assert(n >= 2, "at least two inputs");
@@ -368,53 +379,75 @@ __device__ __forceinline__ uint32_t opaque_uniform(uint32_t x) {
   return x;
 }
 
-// Maximum over the kMaxWaves per-wave entries at w (16-byte aligned; entries of
-// waves that do not exist hold -inf): four broadcast 16-byte LDS reads, no
-// dependent round trips.
-__device__ __forceinline__ float block_max(const float* w) {
-  static_assert(kMaxWaves == 16, "block_max reads four float4");
-  const float4* w4 = reinterpret_cast<const float4*>(w);
-  const float4 a = w4[0], b = w4[1], c = w4[2], d = w4[3];
-  const float ab = fmaxf(fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w)), fmaxf(fmaxf(b.x, b.y), fmaxf(b.z, b.w)));
-  const float cd = fmaxf(fmaxf(fmaxf(c.x, c.y), fmaxf(c.z, c.w)), fmaxf(fmaxf(d.x, d.y), fmaxf(d.z, d.w)));
-  return fmaxf(ab, cd);
+// ---------------------------------------------------------------------------
+// Wave (64-lane) and block reductions.  Blocks are always a whole number of
+// waves; threads without work contribute the neutral element.
+// ---------------------------------------------------------------------------
+// DPP move of v (rows of 16 lanes: quad_perm, row mirrors; or row broadcasts
+// under a row mask); rows the mask leaves out read `old`.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp_i(int old, int v) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWS, 0xF, false);
 }
-
-// ---------------------------------------------------------------------------
-// Wave (64-lane) reductions.  Blocks are always a whole number of waves;
-// threads without work contribute the neutral element.
-// ---------------------------------------------------------------------------
-// DPP move of v within rows of 16 lanes (CTRL: quad_perm, row mirrors).
-template <int CTRL>
-__device__ __forceinline__ float dpp_row(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+  return __builtin_bit_cast(float, dpp_i<CTRL, ROWS>(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v)));
 }
 
 constexpr int kDppSwap1 = 0xB1;       // quad_perm [1, 0, 3, 2]
 constexpr int kDppSwap2 = 0x4E;       // quad_perm [2, 3, 0, 1]
 constexpr int kDppHalfMirror = 0x141; // row_half_mirror
 constexpr int kDppMirror = 0x140;     // row_mirror
+constexpr int kDppBcast15 = 0x142;    // lane 15 of each row to the next row (rows 1, 3: mask 0xA)
+constexpr int kDppBcast31 = 0x143;    // lane 31 to rows 2 and 3 (mask 0xC)
 
-__device__ __forceinline__ float lane_of(float v, int l) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+// Order-preserving integer key of a float that is not NaN (-inf included):
+// signed comparison of keys orders the floats, so maxima reduce with
+// v_max_i32, whose DPP forms take the move for free (the float max would
+// quiet each DPP operand first).
+__device__ __forceinline__ int fkey(float v) {
+  const int b = __builtin_bit_cast(int, v);
+  return b ^ ((b >> 31) & 0x7fffffff);
+}
+__device__ __forceinline__ float fkey_inv(int k) { return __builtin_bit_cast(float, k ^ ((k >> 31) & 0x7fffffff)); }
+
+// The 16 lanes of each row end with the row's maximum key.
+__device__ __forceinline__ int row_max_key(int k) {
+  k = max(k, dpp_i<kDppSwap1>(INT_MIN, k));
+  k = max(k, dpp_i<kDppSwap2>(INT_MIN, k));
+  k = max(k, dpp_i<kDppHalfMirror>(INT_MIN, k));
+  return max(k, dpp_i<kDppMirror>(INT_MIN, k));
 }
 
-// Wave results are uniform: four DPP steps leave each row's reduction in every
-// lane of the row, and four readlanes combine the rows.
+// Maximum over the wave (v not NaN; -inf for lanes without work), uniform:
+// the row maxima, then two row broadcasts leave the wave's in lane 63.
 __device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, dpp_row<kDppSwap1>(v));
-  v = fmaxf(v, dpp_row<kDppSwap2>(v));
-  v = fmaxf(v, dpp_row<kDppHalfMirror>(v));
-  v = fmaxf(v, dpp_row<kDppMirror>(v));
-  return fmaxf(fmaxf(lane_of(v, 0), lane_of(v, 16)), fmaxf(lane_of(v, 32), lane_of(v, 48)));
+  int k = row_max_key(fkey(v));
+  k = max(k, dpp_i<kDppBcast15, 0xA>(INT_MIN, k));
+  k = max(k, dpp_i<kDppBcast31, 0xC>(INT_MIN, k));
+  return fkey_inv(__builtin_amdgcn_readlane(k, 63));
 }
 
+// Maximum over the kMaxWaves = 16 per-wave entries at w (entries of waves
+// that do not exist hold -inf), uniform: every row of a wave reads the 16
+// entries and reduces them.
+__device__ __forceinline__ float block_max(const float* w) {
+  static_assert(kMaxWaves == 16, "one entry per lane of a row");
+  const int k = row_max_key(fkey(w[threadIdx.x & 15]));
+  return fkey_inv(__builtin_amdgcn_readfirstlane(k));
+}
+
+// Sum over the wave, uniform: the row sums (four DPP steps), then row 1 +=
+// row 0 and row 3 += row 2, then row 3 += row 1, i.e. (r3 + r2) + (r1 + r0).
+// -0 is the identity the rows a broadcast leaves out read.
 __device__ __forceinline__ float wave_sum(float v) {
-  v += dpp_row<kDppSwap1>(v);
-  v += dpp_row<kDppSwap2>(v);
-  v += dpp_row<kDppHalfMirror>(v);
-  v += dpp_row<kDppMirror>(v);
-  return (lane_of(v, 0) + lane_of(v, 16)) + (lane_of(v, 32) + lane_of(v, 48));
+  v += dpp_f<kDppSwap1>(0.0f, v);
+  v += dpp_f<kDppSwap2>(0.0f, v);
+  v += dpp_f<kDppHalfMirror>(0.0f, v);
+  v += dpp_f<kDppMirror>(0.0f, v);
+  v += dpp_f<kDppBcast15, 0xA>(-0.0f, v);
+  v += dpp_f<kDppBcast31, 0xC>(-0.0f, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // ---------------------------------------------------------------------------

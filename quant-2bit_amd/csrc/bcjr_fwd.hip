@@ -227,9 +227,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
           }
           float M = 0.0f;
           if constexpr (SHIFT) {
-            M = a[0];
-#pragma unroll
-            for (int p = 1; p < R; ++p) M = fmaxf(M, a[p]);
+            M = max_of_inputs(a);
           }
           float s = fexp2(a[0] - M);
 #pragma unroll
@@ -288,8 +286,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
                 }
               }
               store_vec<R>(cur + R * u, mo);
-#pragma unroll
-              for (int r = 0; r < R; ++r) tmax = fmaxf(tmax, mo[r]);
+              tmax = max_with(tmax, mo);
             } else if constexpr (kColUnroll) {
               // Outputs unrolled, so every state's LUT offset is an immediate;
               // a butterfly with an underflowed group is redone output by output.
@@ -301,7 +298,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
                 const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, cbs[r]);
                 smin = r ? fminf(smin, s) : s;
                 cur[R * u + (r ^ fu)] = mo;
-                tmax = fmaxf(tmax, mo);
+                tmax = vmax_raw(tmax, mo);
               }
               if constexpr (!EXACT) {
                 if (smin < kUnderflow) {
@@ -310,7 +307,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
                     float mo;
                     alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo, hyb_col_base((uint32_t)(R * u + r), P.Q));
                     cur[R * u + (r ^ fu)] = mo;
-                    tmax = fmaxf(tmax, mo);
+                    tmax = vmax_raw(tmax, mo);
                   }
                 }
               }
@@ -322,7 +319,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
                 const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, cb);
                 if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo, cb);
                 cur[R * u + r] = mo;
-                tmax = fmaxf(tmax, mo);
+                tmax = vmax_raw(tmax, mo);
               }
             }
           }
@@ -415,9 +412,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
           }
           float M = 0.0f;
           if constexpr (SHIFT) {
-            M = y[0];
-#pragma unroll
-            for (int c = 1; c < R; ++c) M = fmaxf(M, y[c]);
+            M = max_of_inputs(y);
           }
           float e[R], s = 0.0f, ec[V];
 #pragma unroll
@@ -523,8 +518,8 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 #pragma unroll
               for (int p = 0; p < R; ++p) {
                 cur[p * NB + u] = no[p];
-                tmax = fmaxf(tmax, no[p]);
               }
+              tmax = max_with(tmax, no);
             } else if constexpr (kColUnroll) {
               // Outputs unrolled, so every state's LUT offset is an immediate;
               // the butterfly's sums are redone when a group underflowed.
@@ -542,7 +537,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
                 for (int v = 0; v < V; ++v) ua[v] += cs[v];
                 uh += hs;
                 cur[p * NB + u] = no;
-                tmax = fmaxf(tmax, no);
+                tmax = vmax_raw(tmax, no);
               }
               if constexpr (!EXACT) {
                 if (smin < kUnderflow) {
@@ -558,7 +553,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
                     for (int v = 0; v < V; ++v) ua[v] += cs[v];
                     uh += hs;
                     cur[p * NB + u] = no;
-                    tmax = fmaxf(tmax, no);
+                    tmax = vmax_raw(tmax, no);
                   }
                 }
               }
@@ -578,7 +573,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
                 for (int v = 0; v < V; ++v) acc[v] += cs[v];
                 hacc += hs;
                 cur[p * NB + u] = no;
-                tmax = fmaxf(tmax, no);
+                tmax = vmax_raw(tmax, no);
               }
             }
           }

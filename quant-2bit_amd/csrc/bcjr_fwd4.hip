@@ -41,8 +41,6 @@ __device__ __forceinline__ double uniform_d(double x) {
   return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
-__device__ __forceinline__ float max4(const float (&v)[4]) { return fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])); }
-
 // f(0) ... f(UPT - 1): unrolled, or as a loop (one unit's registers reused).
 template <bool ROLLED, int UPT, typename F>
 __device__ __forceinline__ void for_units(F&& f) {
@@ -187,7 +185,7 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
                 const float d = fmaf(hv(i, p, r), ssk, nw);
                 a[p] = fmaf(-d, d, m[p]);
               }
-              const float Ma = max4(a);
+              const float Ma = max_of_inputs(a);
               float s = fexp2(a[0] - Ma);
 #pragma unroll
               for (int p = 1; p < R; ++p) s += fexp2(a[p] - Ma);
@@ -220,7 +218,7 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
                   const float d = fmaf(hv(i, p, r), ssk, nwx);
                   a[p] = fmaf(-d, d, m[p]);
                 }
-                const float Ma = max4(a);
+                const float Ma = max_of_inputs(a);
                 float s = fexp2(a[0] - Ma);
 #pragma unroll
                 for (int p = 1; p < R; ++p) s += fexp2(a[p] - Ma);
@@ -229,7 +227,7 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
             }
           }
           store_vec<R>(cur + R * u, mo);
-          tmax = fmaxf(tmax, max4(mo));
+          tmax = max_with(tmax, mo);
         });
         __builtin_amdgcn_sched_barrier(0);
         tmax = wave_max(tmax);
@@ -314,7 +312,7 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
                 const float d = fmaf(hv(i, p, c), ssk, nw);
                 y[c] = fmaf(-d, d, n[c]);
               }
-              const float My = max4(y);
+              const float My = max_of_inputs(y);
               float s = 0.0f, ec = 0.0f;
 #pragma unroll
               for (int c = 0; c < R; ++c) {
@@ -356,7 +354,7 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
                   const float d = fmaf(hv(i, p, c), ssk, nwx);
                   y[c] = fmaf(-d, d, n[c]);
                 }
-                const float My = max4(y);
+                const float My = max_of_inputs(y);
                 float s = 0.0f, ec = 0.0f;
 #pragma unroll
                 for (int c = 0; c < R; ++c) {
@@ -372,7 +370,7 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
           acc += ua;
 #pragma unroll
           for (int p = 0; p < R; ++p) cur[p * NB + u] = no[p];
-          tmax = fmaxf(tmax, max4(no));
+          tmax = max_with(tmax, no);
         });
         __builtin_amdgcn_sched_barrier(0);
         D = uniform_d(D + (double)Qv);
