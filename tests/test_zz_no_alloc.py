@@ -2,8 +2,13 @@
 bcjr_forward through the C ABI: two calls in a row, the second with a smaller
 input, each bit-identical to the allocating entry point's output (the same
 kernel runs every sequence independently; only the number of slots differs).
-Also: a problem whose slot exceeds the static array is refused."""
+Also: a problem whose slot exceeds the static array is refused, and the array
+is reserved on a GPU only by the first no-alloc call there, not by loading the
+library or by the other entry points."""
 import ctypes
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -71,3 +76,57 @@ def test_noalloc_refuses_a_slot_larger_than_the_array(bcjr_mod):
                                   d.data_ptr(), None)
     assert rc == _lib.BCJR_EWORKSPACE
     assert "static scratch holds 134217728" in lib.bcjr_last_error().decode()
+
+
+# Run in a fresh process, so that no earlier test has called the no-alloc entry
+# point: device memory free before and after a bcjr_forward, then after the
+# first and a second bcjr_forward_noalloc, with every tensor allocated first.
+_RESERVE_PROBE = r"""
+import ctypes, sys
+sys.path.insert(0, sys.argv[1])
+import torch
+from bcjr import _lib
+dev = torch.device("cuda")
+def free():
+    torch.cuda.synchronize()
+    return torch.cuda.mem_get_info(dev)[0]
+lib = _lib.load()
+L, N, B = 12, 64, 4
+prob = _lib.Problem(L, 2, 1, B, N, _lib.CODE_1MAD, 9, 0)
+x = torch.randn(B, N, 1, device=dev)
+T = torch.full((1,), 0.2, device=dev)
+soft, logZ = torch.empty_like(x), torch.empty(B, device=dev)
+n = ctypes.c_size_t(0)
+_lib.check(lib.bcjr_workspace_bytes(ctypes.byref(prob), 0, ctypes.byref(n)), "ws")
+ws = torch.empty(n.value, dtype=torch.uint8, device=dev)
+s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+f0 = free()
+_lib.check(lib.bcjr_forward(ctypes.byref(prob), x.data_ptr(), T.data_ptr(), None, soft.data_ptr(),
+                            logZ.data_ptr(), ws.data_ptr(), ws.numel(), s), "forward")
+f1 = free()
+def noalloc():
+    _lib.check(lib.bcjr_forward_noalloc(ctypes.byref(prob), x.data_ptr(), T.data_ptr(), None,
+                                        soft.data_ptr(), logZ.data_ptr(), s), "forward_noalloc")
+noalloc()
+f2 = free()
+noalloc()
+f3 = free()
+print("RESERVED", f0 - f1, f1 - f2, f2 - f3, flush=True)
+"""
+
+
+def test_noalloc_array_reserved_by_its_first_call():
+    if os.environ.get("HIP_ENABLE_DEFERRED_LOADING", "1") == "0":
+        pytest.skip("code objects load eagerly in this environment")
+    pkg = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "quant-2bit_amd")
+    _say("fresh process: free device memory around forward and two no-alloc calls")
+    out = subprocess.run([sys.executable, "-c", _RESERVE_PROBE, pkg], capture_output=True, text=True,
+                         timeout=240)
+    assert out.returncode == 0, out.stderr[-2000:]
+    line = [ln for ln in out.stdout.splitlines() if ln.startswith("RESERVED")][-1]
+    fwd, first, second = (int(v) for v in line.split()[1:])
+    _say(f"forward {fwd >> 20} MiB, first no-alloc call {first >> 20} MiB, second {second >> 20} MiB")
+    scratch = 128 << 20
+    assert fwd < scratch // 4  # the allocating forward does not load the array
+    assert first >= scratch  # the first no-alloc call does
+    assert second < scratch // 4  # and later calls reuse it
