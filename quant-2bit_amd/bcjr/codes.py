@@ -20,6 +20,7 @@ examined and takes the table kernels.
 """
 from __future__ import annotations
 
+import warnings
 import weakref
 
 import numpy as np
@@ -71,6 +72,8 @@ def code_of(codebook: torch.Tensor) -> int:
 
 # id(storage) -> (weakref to it, (offset, shape, stride, dtype), version, (code, Q, lut or None))
 _SEEN: dict = {}
+# Storages for which the capture warning of resolve_codebook was given.
+_CAPTURE_WARNED = weakref.WeakSet()
 # (device, code, L) -> generated codebook, for the comparisons
 _GENERATED: dict = {}
 # (L, Q) -> (rep_state (2^Q,) int64 or -1, negate (2^Q,) bool): for every LUT
@@ -196,6 +199,15 @@ def resolve_codebook(codebook: torch.Tensor, L: int, k: int, V: int, device: tor
             res = r
     if res is None:
         if torch.cuda.is_current_stream_capturing():
+            # Recognition compares on the device and reads the verdict back, which
+            # a capture cannot do: the table runs on the table kernels (correct,
+            # but several times slower than the generator kernels at L = 16).
+            if storage not in _CAPTURE_WARNED:
+                _CAPTURE_WARNED.add(storage)
+                warnings.warn(
+                    "bcjr: a codebook table first seen inside a graph capture runs on the table kernels; "
+                    "call the node (or bcjr.codes.resolve_codebook) on it once before capturing so that a "
+                    "1MAD/3INST/HYB table reaches its generator kernels", RuntimeWarning, stacklevel=3)
             return Spec(L, k, V, CODE_TABLE), table
         res = _recognise(table, L, V)
         for dead in [k_ for k_, v in _SEEN.items() if v[0]() is None]:

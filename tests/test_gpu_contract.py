@@ -190,6 +190,30 @@ def test_python_float_T_graph_capture(bcjr_mod):
         _ = float(other.sum())
 
 
+def test_unseen_table_inside_a_capture_warns_and_runs_the_table_kernels(bcjr_mod, oracle):
+    """A 3INST table made without the generator tag and first seen inside a
+    graph capture cannot be recognised there (no read-back): the node warns once
+    and runs the table kernels, whose replays still match the oracle."""
+    _say("unseen table under capture")
+    L, B, N, T = 12, 8, 64, 0.2
+    plain = bcjr_mod.make_3inst_codebook(L, "cuda").clone()
+    assert not hasattr(plain, "_bcjr_code")
+    x = torch.randn(B, N, 1, device="cuda", generator=torch.Generator("cuda").manual_seed(11))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with pytest.warns(RuntimeWarning, match="table kernels"):
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(graph):
+                out, _ = bcjr_mod.bcjr_forward_backward(x, plain, T, L=L, k=2, V=1)
+    torch.cuda.current_stream().wait_stream(s)
+    s_ref, _ = oracle.bcjr_forward(x.cpu().numpy(), plain.cpu().numpy(), T, L, 2)
+    for i in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert max_rel(out.cpu().numpy(), s_ref) < SOFT_TOL, i
+
+
 def test_torch_compile_fullgraph_quantize_weight(bcjr_mod):
     """torch.compile(fullgraph=True) over bcjr_quantize_weight: no graph break;
     values and gradients equal the eager call's (the same kernels run)."""
