@@ -450,6 +450,19 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Sum of the n <= 16 per-wave entries w[0], w[stride], ..., w[(n - 1) stride],
+// uniform over the calling wave: every row of 16 lanes reads them (lanes past n
+// read 0) and adds them pairwise in four DPP steps.
+__device__ __forceinline__ float sum_of_waves(const float* w, int n, int stride) {
+  const int l = (int)(threadIdx.x & 15);
+  float v = l < n ? w[l * stride] : 0.0f;
+  v += dpp_f<kDppSwap1>(0.0f, v);
+  v += dpp_f<kDppSwap2>(0.0f, v);
+  v += dpp_f<kDppHalfMirror>(0.0f, v);
+  v += dpp_f<kDppMirror>(0.0f, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
 // ---------------------------------------------------------------------------
 // Kernel parameter blocks (passed by value).
 // ---------------------------------------------------------------------------

@@ -122,12 +122,20 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
     const float ssk = CT::kSigma * sk;  // d = (c - w) * sk = h * ssk - w * sk
     const float* seqb = P.seq + (size_t)b * N * V;
     float* softb = P.soft + (size_t)b * N * V;
-    // Marginal entropy of step t in nats, -ln 2 * sum_s P log2 P, from the
-    // per-wave sums in partial buffer `par`, summed in wave order.
-    auto entropy_out = [&](int t, int par) {
-      float h = 0.0f;
-      for (int w = 0; w < nwaves; ++w) h += spart[(par * nwaves + w) * SP + V];
-      P.H_out[(size_t)b * N + t] = -h * (float)kLn2;
+    // Soft codeword of step t and, in the diagnostics variant, its marginal
+    // entropy in nats (-ln 2 * sum_s P log2 P), from the per-wave sums in partial
+    // buffer `par`; called by wave 0.
+    auto step_out = [&](int t, int par) {
+      const float* sp = spart + par * nwaves * SP;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float sacc = sum_of_waves(sp + v, nwaves, SP);
+        if (lane == 0) softb[t * V + v] = sacc;
+      }
+      if (INTERNALS && P.H_out) {
+        const float h = sum_of_waves(sp + V, nwaves, SP);
+        if (lane == 0) P.H_out[(size_t)b * N + t] = -h * (float)kLn2;
+      }
     };
     // T must be finite and > 0 and the weights finite; otherwise the sequence's
     // outputs are NaN (the check is one barrier per sequence).
@@ -367,12 +375,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
           Qv = -INFINITY;
           Qv = block_max(wmax + ((k + 1) & 1) * kMaxWaves);
           // soft of step t+1 from its per-wave partials (the other parity buffer)
-          if (tid < V) {
-            float sacc = 0.0f;
-            for (int w = 0; w < nwaves; ++w) sacc += spart[(((k + 1) & 1) * nwaves + w) * SP + tid];
-            softb[(t + 1) * V + tid] = sacc;
-          }
-          if (INTERNALS && tid == V && P.H_out) entropy_out(t + 1, (k + 1) & 1);
+          if (wave == 0) step_out(t + 1, (k + 1) & 1);
         }
         const float Kt = (float)(cvec[t] + D - logZ2);
         float nw[V];
@@ -601,12 +604,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 
     // soft of step 0: its partials sit in the buffer of the last beta step's parity
     const int par0 = (2 * N - 1) & 1;  // k after N alpha and N beta steps, minus one
-    if (tid < V) {
-      float sacc = 0.0f;
-      for (int w = 0; w < nwaves; ++w) sacc += spart[(par0 * nwaves + w) * SP + tid];
-      softb[tid] = sacc;
-    }
-    if (INTERNALS && tid == V && P.H_out) entropy_out(0, par0);
+    if (wave == 0) step_out(0, par0);
     if (tid == 0 && P.logZ) P.logZ[b] = (float)(logZ2 * kLn2);
     if (tid == 0) *bflag = 0;  // every thread read it after the first barrier
     __syncthreads();

@@ -269,10 +269,9 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
         float Qv = 0.0f;
         if (t != N - 1) {
           Qv = uniform_f(block_max(wmax + ((k + 1) & 1) * kMaxWaves));
-          if (tid == 0) {  // soft of step t+1 from its per-wave partials, in wave order
-            float s = 0.0f;
-            for (int w = 0; w < kMaxWaves; ++w) s += spart[((k + 1) & 1) * kMaxWaves + w];
-            softb[t + 1] = s;
+          if (wave == 0) {  // soft of step t+1 from its per-wave partials
+            const float s = sum_of_waves(spart + ((k + 1) & 1) * kMaxWaves, kMaxWaves, 1);
+            if (lane == 0) softb[t + 1] = s;
           }
         }
         const float Kt = uniform_f((float)(cvec[t] + D - logZ2));
@@ -385,12 +384,13 @@ __global__ __launch_bounds__(1024) void bcjr_fwd4_kernel(FwdParams P) {
     const double logZ2 = Tb < kExactBelowTFwd4 ? sweeps(std::true_type{}) : sweeps(std::false_type{});
 
     // soft of step 0: the last beta step (k = 2N - 1, odd) wrote buffer 1
-    if (tid == 0) {
-      float s = 0.0f;
-      for (int w = 0; w < kMaxWaves; ++w) s += spart[kMaxWaves + w];
-      softb[0] = s;
-      if (P.logZ) P.logZ[b] = (float)(logZ2 * kLn2);
-      *bflag = 0;  // every thread read it after the first barrier
+    if (wave == 0) {
+      const float s = sum_of_waves(spart + kMaxWaves, kMaxWaves, 1);
+      if (lane == 0) {
+        softb[0] = s;
+        if (P.logZ) P.logZ[b] = (float)(logZ2 * kLn2);
+        *bflag = 0;  // every thread read it after the first barrier
+      }
     }
     __syncthreads();
   }
