@@ -71,6 +71,11 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "bcjr_layer_hbm_traffic.txt")
 CALIB_BYTES = 256 << 20
 
 
+def progress(msg):
+    """A progress line on stderr (the JSON result goes to stdout)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -588,6 +593,7 @@ def main():
         print(json.dumps({"config": args.config, args.config: res}), flush=True)
         return
 
+    progress("layer: building the seven weights")
     layer = Layer(torch, bcjr, dev)
     cells = float(LAYER_SEQS) * 256 * 65536
     stream = torch.cuda.current_stream(dev)
@@ -598,11 +604,13 @@ def main():
         for _ in range(args.warmup):
             layer.step()
         torch.cuda.synchronize(dev)
+        progress(f"layer: {args.warmup} warmup step(s) done")
         t0 = time.perf_counter()
         for _ in range(args.steps):
             layer.step()
         torch.cuda.synchronize(dev)
         ms_step = (time.perf_counter() - t0) / args.steps * 1e3
+        progress(f"layer: {args.steps} timed step(s), {ms_step:.1f} ms per step")
 
     # ---- the step's three launches, one at a time ----
     fwd_s, bwd_s, vit_s = layer_kernels(torch, ops, layer, dev)
@@ -639,14 +647,19 @@ def main():
         "roofline": roofline, "kernels": kernels,
         "peaks_per_s": {k_: v["per_s"] for k_, v in peaks.items()},
     }
+    progress("layer: per-kernel launches done")
     if not args.no_secondary:
-        line["secondary"] = {"tile": tile_config(torch, bcjr, ops, dev, exp_peak),
-                             "qat_shape": qat_shape(torch, bcjr, ops, dev, exp_peak),
-                             "qat_layer": qat_layer(torch, bcjr, ops, dev, exp_peak),
-                             "drop_in": drop_in_chunked(torch, bcjr, dev),
-                             "dequant": dequant_layer(torch, bcjr, ops, dev)}
+        legs = (("tile", lambda: tile_config(torch, bcjr, ops, dev, exp_peak)),
+                ("qat_shape", lambda: qat_shape(torch, bcjr, ops, dev, exp_peak)),
+                ("qat_layer", lambda: qat_layer(torch, bcjr, ops, dev, exp_peak)),
+                ("drop_in", lambda: drop_in_chunked(torch, bcjr, dev)),
+                ("dequant", lambda: dequant_layer(torch, bcjr, ops, dev)))
         if args.experts > 0:
-            line["secondary"]["experts"] = experts_leg(torch, bcjr, dev, args.experts)
+            legs += (("experts", lambda: experts_leg(torch, bcjr, dev, args.experts)),)
+        line["secondary"] = {}
+        for name, leg in legs:
+            line["secondary"][name] = leg()
+            progress(f"secondary {name} done")
     calibration_copy(torch, dev)
     if not args.no_cpu_baseline:
         x = layer.tiles()
@@ -656,6 +669,7 @@ def main():
         tiles_T = layer.T_tiles[rows].cpu().numpy()
         tiles_g = np.random.default_rng(1).standard_normal(tiles_np.shape).astype(np.float32)
         del x
+        progress("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(args, tiles_np, tiles_T, tiles_g)
     print(json.dumps(line), flush=True)
 
