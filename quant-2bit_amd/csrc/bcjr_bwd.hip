@@ -90,6 +90,10 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   const uint32_t ANT = opaque_uniform(CT::A * (uint32_t)NT);  // hash offset of p * NT
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
+  // The column-walk instance gives thread tid butterfly col_walk_unit(tid), so
+  // that a half-wave's LUT reads hit distinct banks (the host picks the state
+  // swizzle for that lane map); elsewhere u = tid.
+  const int utid = kColUnroll ? (int)col_walk_unit((uint32_t)tid) : tid;
   const Swizzle swz = P.swz;
 
   // LDS: the (m~, mu) pairs sit at byte 0, so a pair's byte address is 8 times
@@ -115,12 +119,12 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
     __syncthreads();
   }
   const unsigned char* lutb = reinterpret_cast<const unsigned char*>(lut);
-  // Column-walk bases of this thread's butterfly u = tid, input c (state R*u + c),
+  // Column-walk bases of this thread's butterfly u = utid, input c (state R*u + c),
   // for the beta sweep; the alpha sweep forms its output's base as it goes.
   uint32_t cbs[kCol ? R : 1];
   if constexpr (kCol) {
 #pragma unroll
-    for (int c = 0; c < R; ++c) cbs[c] = hyb_col_base((uint32_t)(R * min(tid, NB - 1) + c), P.Q);
+    for (int c = 0; c < R; ++c) cbs[c] = hyb_col_base((uint32_t)(R * min(utid, NB - 1) + c), P.Q);
   }
 
   // Raw codewords h of this thread's first NC butterflies (hcx[i][p][c] for
@@ -133,7 +137,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
     constexpr int NC = decltype(count_tag)::value;
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
-      const int u = min(opaque(tid) + i * nthr, NB - 1);
+      const int u = min(opaque(utid) + i * nthr, NB - 1);
       const uint32_t xu = CT::A * (uint32_t)(R * u) + CT::B;
 #pragma unroll
       for (int p = 0; p < R; ++p)
@@ -144,12 +148,12 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
     }
   };
 
-  // Byte address of slot k of butterfly tid + i*nthr at rotation rho:
-  // 8 S(rotr(tid + i*nthr + k*NB)) = yb ^ unit_off(i) ^ slot_off(k), the last
-  // two uniform (tid, i*nthr and k*NB occupy disjoint bits; S and rotr are
+  // Byte address of slot k of butterfly utid + i*nthr at rotation rho:
+  // 8 S(rotr(utid + i*nthr + k*NB)) = yb ^ unit_off(i) ^ slot_off(k), the last
+  // two uniform (utid, i*nthr and k*NB occupy disjoint bits; S and rotr are
   // linear).
   auto base_off = [&](int rho) -> uint32_t {
-    return swizzle(rotr_bits((uint32_t)min(tid, NB - 1), rho, nb), swz) << 3;
+    return swizzle(rotr_bits((uint32_t)min(utid, NB - 1), rho, nb), swz) << 3;
   };
   auto unit_off = [&](int i, int rho) -> uint32_t {
     return swizzle(rotr_bits((uint32_t)(i * nthr), rho, nb), swz) << 3;
@@ -312,7 +316,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         float tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
-          const int q = tid + i * nthr;
+          const int q = utid + i * nthr;
           float mi[R], mui[R];
 #pragma unroll
           for (int p = 0; p < R; ++p) {
@@ -431,7 +435,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
       // Raw alpha-side inputs (m~, mu) of step t come back from HBM two
       // butterflies ahead of their use, across step boundaries.
       auto slot_src = [&](int t, int i) {
-        const int q = min(tid + i * nthr, NB - 1);
+        const int q = min(utid + i * nthr, NB - 1);
         return slot + ((size_t)t * NB + q) * 2 * R;
       };
       // The next two butterflies in consumption order (t descending, i
@@ -562,7 +566,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         float tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
-          const int q = tid + i * nthr;
+          const int q = utid + i * nthr;
           float pm[R], pmu[R], ni[R], nui[R];
 #pragma unroll
           for (int r = 0; r < R; ++r) {

@@ -264,6 +264,13 @@ bcjr::Swizzle pick_swizzle(int L, int KV) {
   return best;
 }
 
+// State layout of the column-walk backward instance (L = 16, kV = 4), whose
+// thread tid holds butterfly col_walk_unit(tid) rather than tid: with this
+// swizzle every half-wave's 64-bit reads and every quarter-wave's 64-bit writes
+// of S(rotr(k*NB + u, rho)) fall in distinct banks over all 256 lanes, the 16
+// slots and the rotations 0, 4, 8 (the search above assumes u = tid).
+constexpr bcjr::Swizzle kColWalkSwizzle = {{4, 6, 8, 31}, {3u, 31u, 15u, 0u}};
+
 int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan* pl) {
   const int KV = p->k * p->V, R = 1 << KV, RO = R < 4 ? R : 4;
   pl->KV = KV;
@@ -331,7 +338,7 @@ int make_plan_uncached(const bcjr_problem* p, int op, const DeviceInfo& di, Plan
     pl->slot_bytes = slot_bytes_of(p, fwd ? OP_FWD : OP_VIT);
   } else {
     pl->cache = false;
-    pl->swz = pick_swizzle(p->L, KV);
+    pl->swz = kcode == bcjr::CODE_HYB_COL ? kColWalkSwizzle : pick_swizzle(p->L, KV);
     pl->fn = bcjr::bwd_kernel_ptr(KV, p->V, kcode, upt);
     pl->lds = bcjr::bwd_lds_bytes(p->L, KV, p->V, N, nwaves, kcode, p->Q);
     pl->slot_bytes = slot_bytes_of(p, OP_BWD);

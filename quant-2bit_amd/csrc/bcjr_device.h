@@ -122,6 +122,31 @@ __device__ __forceinline__ float2 hyb_col_read(const unsigned char* lutb, uint32
   return *reinterpret_cast<const float2*>(lutb + off);
 }
 
+// Butterfly of thread tid in the column-walk soft kernels (256 threads, one
+// 16-state butterfly each).  The LUT column of state 16u + c is bits [6, 11) of
+// x = s^2 + s for Q = 9 (the reference's LUT), the column's low five bits its
+// bank for an 8-byte read by a half-wave.  Over each coset of span(bits 2..6 of
+// u) those banks are a permutation of the 32 banks, for every c (checked over
+// all 256 butterflies in tests/test_capi_cpu.py), so a half-wave owns one coset:
+// u takes tid's bits 0..4 as its bits 2..6, tid's bits 5, 6 as its bits 0, 1,
+// and keeps bit 7.  (A smaller Q has fewer than 32 columns.)
+__host__ __device__ constexpr uint32_t col_walk_unit(uint32_t tid) {
+  return ((tid >> 5) & 3u) | ((tid & 31u) << 2) | (tid & 128u);
+}
+
+// LDS layouts of the column-walk forward's reduced state j (12 bits, element
+// E(j)), conflict-free under col_walk_unit for the accesses of each sweep:
+// alpha reads j = 256p + u (one per p, 64 lanes, 4-byte banks mod 64) and writes
+// j = 16u + r (half-waves, mod 32); beta reads j = 16u + c (mod 64) and writes
+// j = 256p + u (mod 32).  Both are linear bijections with E(c) = c for c < 16,
+// so E(16u + c) = E(16u) ^ c and E(256p + u) = 256p + (E(u) ^ E(256p) mod 256).
+__host__ __device__ constexpr uint32_t col_walk_alpha_el(uint32_t j) {
+  return j ^ ((j >> 5) & 3u) ^ ((j >> 6) & 31u);
+}
+__host__ __device__ constexpr uint32_t col_walk_beta_el(uint32_t j) {
+  return j ^ ((j >> 5) & 3u) ^ ((j >> 7) & 15u) ^ ((j >> 1) & 32u);
+}
+
 // Any state from the column-walk LUT (rows 0..15).
 __device__ __forceinline__ void code_hyb_col(uint32_t s, const float2* lut2c, int Q, float& c0, float& c1) {
   const uint32_t x = __umul24(s, s) + s;

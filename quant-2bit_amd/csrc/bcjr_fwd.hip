@@ -62,6 +62,10 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   const uint32_t ANT = opaque_uniform(CT::A * (uint32_t)NT);  // hash offset of p * NT
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
+  // The column-walk instance gives thread tid butterfly col_walk_unit(tid), so
+  // that a half-wave's LUT reads hit distinct banks, and lays its alpha and beta
+  // state vectors out by col_walk_alpha_el / col_walk_beta_el; elsewhere u = tid.
+  const int utid = kColUnroll ? (int)col_walk_unit((uint32_t)tid) : tid;
 
   double* cvec = reinterpret_cast<double*>(smem);                // N    C_{t-1}
   float* mbuf = reinterpret_cast<float*>(cvec + ((N + 1) & ~1));  // 2*NT reduced state (16-B aligned)
@@ -86,12 +90,12 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
     __syncthreads();
   }
   const unsigned char* lutb = reinterpret_cast<const unsigned char*>(lut);
-  // Column-walk bases of this thread's butterfly u = tid, input c (state R*u + c),
+  // Column-walk bases of this thread's butterfly u = utid, input c (state R*u + c),
   // for the beta sweep; the alpha sweep forms its output's base as it goes.
   uint32_t cbs[kCol ? R : 1];
   if constexpr (kCol) {
 #pragma unroll
-    for (int c = 0; c < R; ++c) cbs[c] = hyb_col_base((uint32_t)(R * min(tid, NB - 1) + c), P.Q);
+    for (int c = 0; c < R; ++c) cbs[c] = hyb_col_base((uint32_t)(R * min(utid, NB - 1) + c), P.Q);
   }
 
   // Raw codewords h of this thread's first CU butterflies, fixed for the
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   if constexpr (CU > 0) {
 #pragma unroll
     for (int i = 0; i < CU; ++i) {
-      const int u = min(tid + i * nthr, NB - 1);
+      const int u = min(utid + i * nthr, NB - 1);
       const uint32_t xu = CT::A * (uint32_t)(R * u) + CT::B;
 #pragma unroll
       for (int p = 0; p < R; ++p)
@@ -244,18 +248,17 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
           return s;
         };
 
-        // Inputs of butterfly tid + i*nthr; the next butterfly's are read
+        // Inputs of butterfly utid + i*nthr; the next butterfly's are read
         // before the current one's arithmetic (prev is read-only this step).
         // The column-walk instance keeps the reduced alpha state j at element
-        // j ^ ((j >> 5) & 15), so that its per-lane stores of 16 consecutive
-        // states (R*u + r) spread over the banks; for the reads j = p*NB + u
-        // (NB = 256) the XOR is (u >> 5) | 8 (p & 1), one base per parity.
+        // col_walk_alpha_el(j), whose low six bits for j = p*NB + u (NB = 256)
+        // are those of E(u) ^ E(256p).
         auto read_in = [&](int i, float (&m)[R]) {
-          const int qq = min(tid + i * nthr, NB - 1);
+          const int qq = min(utid + i * nthr, NB - 1);
           if constexpr (kColUnroll) {
-            const int q0 = qq ^ (qq >> 5), q1 = q0 ^ 8;
+            const uint32_t eu = col_walk_alpha_el((uint32_t)qq);
 #pragma unroll
-            for (int p = 0; p < R; ++p) m[p] = prev[p * NB + ((p & 1) ? q1 : q0)];
+            for (int p = 0; p < R; ++p) m[p] = prev[p * NB + (eu ^ (col_walk_alpha_el((uint32_t)p << 8) & 255u))];
           } else {
 #pragma unroll
             for (int p = 0; p < R; ++p) m[p] = prev[p * NB + qq];
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
         float tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
-          const int q = tid + i * nthr;
+          const int q = utid + i * nthr;
           float m[R];
 #pragma unroll
           for (int p = 0; p < R; ++p) m[p] = nx[p];
@@ -299,13 +302,13 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
               // Outputs unrolled, so every state's LUT offset is an immediate;
               // a butterfly with an underflowed group is redone output by output.
               float smin = 0.0f;
-              const int fu = (u >> 1) & (R - 1);  // the store XOR of state R*u + r
+              const uint32_t e16 = col_walk_alpha_el((uint32_t)(R * u));  // element of state R*u + r: e16 ^ r
 #pragma unroll
               for (int r = 0; r < R; ++r) {
                 float mo;
                 const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, cbs[r]);
                 smin = r ? fminf(smin, s) : s;
-                cur[R * u + (r ^ fu)] = mo;
+                cur[e16 ^ (uint32_t)r] = mo;
                 tmax = vmax_raw(tmax, mo);
               }
               if constexpr (!EXACT) {
@@ -314,7 +317,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
                   for (int r = 0; r < R; ++r) {
                     float mo;
                     alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo, hyb_col_base((uint32_t)(R * u + r), P.Q));
-                    cur[R * u + (r ^ fu)] = mo;
+                    cur[e16 ^ (uint32_t)r] = mo;
                     tmax = vmax_raw(tmax, mo);
                   }
                 }
@@ -358,7 +361,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
       // their use, across step boundaries (the next two in consumption order:
       // t descending, i ascending).
       auto slot_src = [&](int t, int i) {
-        const int q = min(tid + i * nthr, NB - 1);
+        const int q = min(utid + i * nthr, NB - 1);
         return slot + ((size_t)t * NB + q) * R;
       };
       float pa[R], pb[R];
@@ -452,7 +455,17 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
           return s;
         };
 
-        auto read_in = [&](int i, float (&n)[R]) { load_vec<R>(prev + R * min(tid + i * nthr, NB - 1), n); };
+        // The column-walk instance reads state R*u + c at col_walk_beta_el(R*u) ^ c.
+        auto read_in = [&](int i, float (&n)[R]) {
+          const int qq = min(utid + i * nthr, NB - 1);
+          if constexpr (kColUnroll) {
+            const uint32_t f16 = col_walk_beta_el((uint32_t)(R * qq));
+#pragma unroll
+            for (int c = 0; c < R; ++c) n[c] = prev[f16 ^ (uint32_t)c];
+          } else {
+            load_vec<R>(prev + R * qq, n);
+          }
+        };
         float nx[R];
         read_in(0, nx);
         float acc[V], hacc = 0.0f;
@@ -461,7 +474,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
         float tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
-          const int q = tid + i * nthr;
+          const int q = utid + i * nthr;
           float pm[R], n[R];
 #pragma unroll
           for (int r = 0; r < R; ++r) {
@@ -527,6 +540,8 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
               // Outputs unrolled, so every state's LUT offset is an immediate;
               // the butterfly's sums are redone when a group underflowed.
               const float* src = slot_src(t, i);
+              // element of state p*NB + u: p*NB + (fu ^ low bits of E(256p))
+              const uint32_t fu = col_walk_beta_el((uint32_t)u);
               float smin = 0.0f, ua[V], uh = 0.0f;
 #pragma unroll
               for (int v = 0; v < V; ++v) ua[v] = 0.0f;
@@ -539,7 +554,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 #pragma unroll
                 for (int v = 0; v < V; ++v) ua[v] += cs[v];
                 uh += hs;
-                cur[p * NB + u] = no;
+                cur[p * NB + (fu ^ (col_walk_beta_el((uint32_t)p << 8) & 255u))] = no;
                 tmax = vmax_raw(tmax, no);
               }
               if constexpr (!EXACT) {
@@ -555,7 +570,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 #pragma unroll
                     for (int v = 0; v < V; ++v) ua[v] += cs[v];
                     uh += hs;
-                    cur[p * NB + u] = no;
+                    cur[p * NB + (fu ^ (col_walk_beta_el((uint32_t)p << 8) & 255u))] = no;
                     tmax = vmax_raw(tmax, no);
                   }
                 }
