@@ -81,6 +81,9 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   constexpr bool kCol = CODE == CODE_HYB_COL;  // HYB column walk: one butterfly per thread
   static_assert(!kCol || (KV == 4 && UPT == 1), "the column walk is for L = 16, kV = 4");
   constexpr bool kColUnroll = kCol;  // outputs unrolled: immediate LUT offsets
+  // Its alpha + mu sweep reads each state's emission and path feature from a
+  // per-step table (below).
+  constexpr bool kETab = kColUnroll;
 
   extern __shared__ __align__(16) unsigned char smem[];
   const int L = P.L, N = P.N;
@@ -114,11 +117,43 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   if constexpr (CODE == CODE_HYB) {
     stage_hyb_signed(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
     __syncthreads();
-  } else if constexpr (kCol) {
+  } else if constexpr (kCol && !kETab) {
     stage_hyb_col(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
     __syncthreads();
   }
   const unsigned char* lutb = reinterpret_cast<const unsigned char*>(lut);
+  // Table of the column-walk alpha + mu sweep, in the LUT's place until the beta
+  // sweep stages the LUT: per step, the float2 at entry k of the column-walk
+  // layout (32 rows of 64, rows 16..31 repeating 0..15) is (-|d|^2, sg . h) of
+  // that LUT entry h, d = h ssk + nw_t, so a state's pair sits at the byte its
+  // codeword has in the LUT.  The kernel runs 256 threads here; thread tid forms
+  // entries tid + 256j (j < 4) and their row copies, reading the codewords from
+  // the (2^Q, 2) table as stage_hyb_col does.
+  auto build_etab = [&](const float (&nw)[V], const float (&sg)[V], float ssk) {
+    const int ncol = 1 << (P.Q - 3), mask = (1 << P.Q) - 1;
+    float h[4][2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = tid + 256 * j, col = k & 63, i = col + ncol * (k >> 6), ie = i & mask;
+      h[j][0] = col < ncol ? P.table[2 * ie] : 0.0f;
+      const float y = col < ncol ? P.table[2 * ie + 1] : 0.0f;
+      h[j][1] = (i >> P.Q) ? -y : y;
+    }
+    float2* et = reinterpret_cast<float2*>(lut);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float e = 0.0f, f = 0.0f;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float d = fmaf(h[j][v], ssk, nw[v]);
+        e = fmaf(-d, d, e);
+        f = fmaf(sg[v], h[j][v], f);
+      }
+      const int k = tid + 256 * j;
+      et[k] = make_float2(e, f);
+      et[k + 1024] = make_float2(e, f);
+    }
+  };
   // Column-walk bases of this thread's butterfly u = utid, input c (state R*u + c),
   // for the beta sweep; the alpha sweep forms its output's base as it goes.
   uint32_t cbs[kCol ? R : 1];
@@ -235,6 +270,10 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           nw[v] = -wbuf[t * V + v] * sk;
           sg[v] = CT::kSigma * gbuf[t * V + v];  // f = g . c = sg . h
         }
+        if constexpr (kETab) {  // every wave has left step t-1's table (barrier at its end)
+          build_etab(nw, sg, ssk);
+          __syncthreads();
+        }
         const uint32_t yb = base_off(rho);
         uint32_t Ku[UPT], Kk[R];  // uniform per step
 #pragma unroll
@@ -260,6 +299,12 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           float a[R], phi[R];
 #pragma unroll
           for (int p = 0; p < R; ++p) {
+            if constexpr (kETab) {
+              const float2 ef = hyb_col_read(lutb, cb + hyb_col_step(p, r));
+              a[p] = m[p] + ef.x;
+              phi[p] = mui[p] + ef.y;
+              continue;
+            }
             float h[V];
             if (i < CUA) {
 #pragma unroll
@@ -399,6 +444,11 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         rho = rho + KV >= nb ? rho + KV - nb : rho + KV;
         __syncthreads();
       }
+
+      // The beta sweep reads codewords: the LUT replaces the table (every wave
+      // has left it at the last alpha step's barrier; the barriers below come
+      // before the first LUT read).
+      if constexpr (kETab) stage_hyb_col(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
 
       // log2 Z and E[F] = sum_j 2^(m_{N-1}(j) - log2 Z) mu_{N-1}(j); m~ and mu of a
       // state share a pair, so the sums run over pairs.

@@ -41,7 +41,8 @@
 namespace bcjr {
 
 template <int KV, int V, int CODE, int UPT, int CU, bool INTERNALS>
-__global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
+__global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_COL && !INTERNALS ? 3 : 1) void bcjr_fwd_kernel(
+    FwdParams P) {
   constexpr int R = 1 << KV;
   // Butterflies of 2 or 4 states run fully unrolled with their slot inputs
   // prefetched in registers; 16-state butterflies loop over outputs (unrolled
@@ -53,6 +54,8 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   static_assert(!kCol || (KV == 4 && UPT == 1), "the column walk is for L = 16, kV = 4");
   // Its outputs are unrolled except in the diagnostics instance, which would spill.
   constexpr bool kColUnroll = kCol && !INTERNALS;
+  // Its alpha sweep reads each state's emission from a per-step table (below).
+  constexpr bool kETab = kColUnroll;
   using CT = CodeTraits<CODE>;
 
   extern __shared__ __align__(16) unsigned char smem[];
@@ -85,11 +88,19 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
   if constexpr (CODE == CODE_HYB) {
     stage_hyb_signed(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
     __syncthreads();
-  } else if constexpr (kCol) {
+  } else if constexpr (kCol && !kETab) {
     stage_hyb_col(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
     __syncthreads();
   }
   const unsigned char* lutb = reinterpret_cast<const unsigned char*>(lut);
+  // Emission table of the column-walk alpha sweep, in the LUT's place until the
+  // beta sweep stages the LUT: per step, entry k of the column-walk layout (32
+  // rows of 64, rows 16..31 repeating 0..15) holds the emission -|d|^2 of that
+  // LUT entry, d = c sk - w_t sk, double-buffered by step parity and interleaved
+  // (entry k of buffer b at float 2k + b).  State s's emission is then the float
+  // at the byte its codeword has in the LUT, plus 4b.  The kernel runs 256
+  // threads here; thread tid forms entries tid + 256j (j < 4) and their row
+  // copies, reading the codewords from the (2^Q, 2) table as stage_hyb_col does.
   // Column-walk bases of this thread's butterfly u = utid, input c (state R*u + c),
   // for the beta sweep; the alpha sweep forms its output's base as it goes.
   uint32_t cbs[kCol ? R : 1];
@@ -184,6 +195,38 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
       using Fast = std::integral_constant<bool, EXACT>;
 
       // ------------------------------ alpha sweep ------------------------------
+      // Emission table of step t into buffer t & 1 (kETab).
+      auto build_etab = [&](int t) {
+        float nwt[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) nwt[v] = -wbuf[t * V + v] * sk;
+        float* et = lut + (t & 1);
+        const int ncol = 1 << (P.Q - 3), mask = (1 << P.Q) - 1;
+        float h[4][2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int k = tid + 256 * j, col = k & 63, i = col + ncol * (k >> 6), ie = i & mask;
+          h[j][0] = col < ncol ? P.table[2 * ie] : 0.0f;
+          const float y = col < ncol ? P.table[2 * ie + 1] : 0.0f;
+          h[j][1] = (i >> P.Q) ? -y : y;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float e = 0.0f;
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const float d = fmaf(h[j][v], ssk, nwt[v]);
+            e = fmaf(-d, d, e);
+          }
+          const int k = tid + 256 * j;
+          et[2 * k] = e;
+          et[2 * (k + 1024)] = e;
+        }
+      };
+      if constexpr (kETab) {
+        build_etab(0);
+        __syncthreads();
+      }
       double C = 0.0;  // C_{t-1}
       int k = 0;       // step counter across both sweeps: LDS buffer / wmax parity
       for (int t = 0; t < N; ++t, ++k) {
@@ -199,6 +242,10 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
         float nw[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) nw[v] = -wbuf[t * V + v] * sk;
+        // The next step's emission table goes to the buffer step t - 1 read,
+        // which every wave has left (barrier at the end of each step).
+        if (kETab && t + 1 < N) build_etab(t + 1);
+        const uint32_t eoff = 4u * (uint32_t)(t & 1);
 
         // Output r of butterfly u (unit i) from the shifted inputs m[p]
         // (maximum 0): returns the group sum, mo = m~_t(R*u + r).
@@ -213,7 +260,9 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
             // The two-rounding d_3inst form is kept out of the low-temperature
             // variant, where |d| reaches ~1e2 and float32 precision is tightest.
             const bool cached = i < CU;
-            if (!cached && CODE == CODE_3INST && !EXACT) {
+            if constexpr (kETab) {
+              acc += *reinterpret_cast<const float*>(lutb + cb + hyb_col_step(p, r));
+            } else if (!cached && CODE == CODE_3INST && !EXACT) {
               const float d = d_3inst(xu + p * ANT + CT::A * (uint32_t)r, ssk, nw[0]);
               acc = fmaf(-d, d, acc);
             } else {
@@ -306,7 +355,7 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 #pragma unroll
               for (int r = 0; r < R; ++r) {
                 float mo;
-                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, cbs[r]);
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, cbs[r] + eoff);
                 smin = r ? fminf(smin, s) : s;
                 cur[e16 ^ (uint32_t)r] = mo;
                 tmax = vmax_raw(tmax, mo);
@@ -316,7 +365,8 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
 #pragma unroll 1
                   for (int r = 0; r < R; ++r) {
                     float mo;
-                    alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo, hyb_col_base((uint32_t)(R * u + r), P.Q));
+                    alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo,
+                              hyb_col_base((uint32_t)(R * u + r), P.Q) + eoff);
                     cur[e16 ^ (uint32_t)r] = mo;
                     tmax = vmax_raw(tmax, mo);
                   }
@@ -339,6 +389,11 @@ __global__ __launch_bounds__(512) void bcjr_fwd_kernel(FwdParams P) {
         if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
         __syncthreads();
       }
+
+      // The beta sweep reads codewords: the LUT replaces the emission table
+      // (every wave has left the table at the last alpha step's barrier; the
+      // barriers below come before the first LUT read).
+      if constexpr (kETab) stage_hyb_col(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
 
       // log2 Z = C_{N-1} + LSE2 over the final reduced state.
       const float* fin = mbuf + ((k + 1) & 1) * NT;
