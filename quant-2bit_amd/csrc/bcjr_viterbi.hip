@@ -95,20 +95,26 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
     }
   };
 
-  if constexpr (kColV) {
+  // Column-walk LUT entry k (row k >> 6 mod 16, column k & 63) as stage_hyb_col
+  // forms it from the (2^Q, 2) table.
+  auto col_entry = [&](int k) -> float2 {
     const int ncol = 1 << (P.Q - 3), mask = (1 << P.Q) - 1;
-    for (int i = tid; i < (32 * 64) << kColRep; i += nthr) {
-      const int k = i >> kColRep, col = k & 63, si = col + ncol * ((k >> 6) & 15);
-      float2 v = make_float2(0.0f, 0.0f);
-      if (col < ncol) {
-        const int e = si & mask;
-        const float y = P.table[2 * e + 1];
-        v = make_float2(P.table[2 * e], (si >> P.Q) ? -y : y);
-      }
-      lut2[i] = v;
+    const int col = k & 63, si = col + ncol * ((k >> 6) & 15);
+    float2 v = make_float2(0.0f, 0.0f);
+    if (col < ncol) {
+      const int e = si & mask;
+      const float y = P.table[2 * e + 1];
+      v = make_float2(P.table[2 * e], (si >> P.Q) ? -y : y);
     }
-    __syncthreads();
-  } else if constexpr (kSignedRep) {
+    return v;
+  };
+  // The column-walk LUT's copies, staged after each sequence's state loop, which
+  // holds per-step cost tables in their place (below), for the final pass and
+  // the traceback.
+  auto stage_col = [&]() {
+    for (int i = tid; i < (32 * 64) << kColRep; i += nthr) lut2[i] = col_entry(i >> kColRep);
+  };
+  if constexpr (kSignedRep) {
     const int nl = (2 << P.Q) << rep, mask = (1 << P.Q) - 1;
     for (int i = tid; i < nl; i += nthr) {
       const int si = i >> rep, e = si & mask;
@@ -163,6 +169,28 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
     const uint32_t ov = cons ? (uint32_t)P.overlap[b] & ((1u << ob) - 1u) : 0u;  // masked as encode.py:136
     for (int j = tid; j < NT; j += nthr)
       rbuf[NT + j] = (cons && ((uint32_t)j >> (L - KV - ob)) != ov) ? kVitInf : 0.0f;
+    // Column walk: the cost E_t of every LUT entry, computed once per step as
+    // the state loop would (same operations and order, so the same float), sits
+    // in the LUT copies' place: entry k's cost of step t is the float at the byte
+    // of its codeword's float2 in each copy, plus 4 (t & 1).  The LUT copies
+    // come back after the loop.
+    auto build_cost = [&](int t) {
+      float* dst = reinterpret_cast<float*>(lut2) + (t & 1);
+      for (int k = tid; k < 16 * 64; k += nthr) {
+        const float2 cv = col_entry(k);
+        const float d0 = cv.x - wbuf[t * V];
+        const float d1 = cv.y - wbuf[t * V + 1];
+        float e = 0.0f;
+        e = e + d0 * d0;
+        e = e + d1 * d1;
+#pragma unroll
+        for (int cp = 0; cp < (1 << kColRep); ++cp) {
+          dst[2 * ((k << kColRep) | cp)] = e;
+          dst[2 * (((k + 16 * 64) << kColRep) | cp)] = e;
+        }
+      }
+    };
+    if constexpr (kColV) build_cost(0);
     __syncthreads();
 
     for (int t = 0; t < N; ++t) {
@@ -171,6 +199,10 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
       float w[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) w[v] = wbuf[t * V + v];
+      // the next step's table goes to the buffer step t - 1 read (every wave
+      // has left it: barrier at the end of each step)
+      if (kColV && t + 1 < N) build_cost(t + 1);
+      const uint32_t eoff = 4u * (uint32_t)(t & 1);
 #pragma unroll
       for (int i = 0; i < UPT; ++i) {
         const int q = tid + i * nthr;
@@ -191,22 +223,22 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
 #pragma unroll
             for (int p = 0; p < R; ++p) {
               float c[V];
-              if constexpr (CACHE) {
-#pragma unroll
-                for (int v = 0; v < V; ++v) c[v] = cw[i][p][r][v];
-              } else if constexpr (kColV) {
-                const float2 cv = hyb_col_read(lutb, cbv[r] + (hyb_col_step(p, sub4 + r) << kColRep));
-                c[0] = cv.x;
-                c[1] = cv.y;
-              } else {
-                cword((uint32_t)(p * NT + R * u + rr), c);
-              }
               float e = 0.0f;
+              if constexpr (kColV) {
+                e = *reinterpret_cast<const float*>(lutb + cbv[r] + (hyb_col_step(p, sub4 + r) << kColRep) + eoff);
+              } else {
+                if constexpr (CACHE) {
 #pragma unroll
-              for (int v = 0; v < V; ++v) {
-                const float d = c[v] - w[v];
-                const float d2 = d * d;
-                e = e + d2;
+                  for (int v = 0; v < V; ++v) c[v] = cw[i][p][r][v];
+                } else {
+                  cword((uint32_t)(p * NT + R * u + rr), c);
+                }
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+                  const float d = c[v] - w[v];
+                  const float d2 = d * d;
+                  e = e + d2;
+                }
               }
               const float cum = ri[p] + e;
               if (p == 0 || cum < best) {
@@ -236,6 +268,11 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
           }
         }
       }
+      __syncthreads();
+    }
+
+    if constexpr (kColV) {  // the LUT copies again (the last step's barrier ended every table read)
+      stage_col();
       __syncthreads();
     }
 
