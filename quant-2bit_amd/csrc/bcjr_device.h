@@ -123,15 +123,15 @@ __device__ __forceinline__ float2 hyb_col_read(const unsigned char* lutb, uint32
 }
 
 // Butterfly of thread tid in the column-walk soft kernels (256 threads, one
-// 16-state butterfly each).  The LUT column of state 16u + c is bits [6, 11) of
-// x = s^2 + s for Q = 9 (the reference's LUT), the column's low five bits its
-// bank for an 8-byte read by a half-wave.  Over each coset of span(bits 2..6 of
-// u) those banks are a permutation of the 32 banks, for every c (checked over
-// all 256 butterflies in tests/test_capi_cpu.py), so a half-wave owns one coset:
-// u takes tid's bits 0..4 as its bits 2..6, tid's bits 5, 6 as its bits 0, 1,
-// and keeps bit 7.  (A smaller Q has fewer than 32 columns.)
+// 16-state butterfly each).  The LUT column of state 16u + c is bits [6, 12) of
+// x = s^2 + s for Q = 9 (the reference's LUT).  Over each coset of span(bits
+// 2..7 of u) those columns are all 64 distinct, for every c, so a wave owns one
+// coset: u takes tid's bits 0..5 as its bits 2..7 and the wave index as its bits
+// 0, 1.  Then a half-wave's 8-byte LUT reads hit 32 distinct banks and a wave's
+// 4-byte reads of a per-step table in the LUT's layout 64 distinct banks
+// (checked in tests/test_capi_cpu.py).  (A smaller Q has fewer columns.)
 __host__ __device__ constexpr uint32_t col_walk_unit(uint32_t tid) {
-  return ((tid >> 5) & 3u) | ((tid & 31u) << 2) | (tid & 128u);
+  return ((tid >> 6) & 3u) | ((tid & 63u) << 2);
 }
 
 // LDS layouts of the column-walk forward's reduced state j (12 bits, element
@@ -140,11 +140,9 @@ __host__ __device__ constexpr uint32_t col_walk_unit(uint32_t tid) {
 // j = 16u + r (half-waves, mod 32); beta reads j = 16u + c (mod 64) and writes
 // j = 256p + u (mod 32).  Both are linear bijections with E(c) = c for c < 16,
 // so E(16u + c) = E(16u) ^ c and E(256p + u) = 256p + (E(u) ^ E(256p) mod 256).
-__host__ __device__ constexpr uint32_t col_walk_alpha_el(uint32_t j) {
-  return j ^ ((j >> 5) & 3u) ^ ((j >> 6) & 31u);
-}
+__host__ __device__ constexpr uint32_t col_walk_alpha_el(uint32_t j) { return j ^ ((j >> 6) & 31u); }
 __host__ __device__ constexpr uint32_t col_walk_beta_el(uint32_t j) {
-  return j ^ ((j >> 5) & 3u) ^ ((j >> 7) & 15u) ^ ((j >> 1) & 32u);
+  return j ^ ((j >> 4) & 3u) ^ ((j >> 6) & 63u);
 }
 
 // Any state from the column-walk LUT (rows 0..15).

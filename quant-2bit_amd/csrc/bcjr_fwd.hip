@@ -66,7 +66,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
   // The column-walk instance gives thread tid butterfly col_walk_unit(tid), so
-  // that a half-wave's LUT reads hit distinct banks, and lays its alpha and beta
+  // that its LUT and emission-table reads hit distinct banks, and lays its alpha and beta
   // state vectors out by col_walk_alpha_el / col_walk_beta_el; elsewhere u = tid.
   const int utid = kColUnroll ? (int)col_walk_unit((uint32_t)tid) : tid;
 
@@ -94,13 +94,14 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   }
   const unsigned char* lutb = reinterpret_cast<const unsigned char*>(lut);
   // Emission table of the column-walk alpha sweep, in the LUT's place until the
-  // beta sweep stages the LUT: per step, entry k of the column-walk layout (32
-  // rows of 64, rows 16..31 repeating 0..15) holds the emission -|d|^2 of that
-  // LUT entry, d = c sk - w_t sk, double-buffered by step parity and interleaved
-  // (entry k of buffer b at float 2k + b).  State s's emission is then the float
-  // at the byte its codeword has in the LUT, plus 4b.  The kernel runs 256
-  // threads here; thread tid forms entries tid + 256j (j < 4) and their row
-  // copies, reading the codewords from the (2^Q, 2) table as stage_hyb_col does.
+  // beta sweep stages the LUT: per step, float k of the table (the column-walk
+  // layout: 32 rows of 64, rows 16..31 repeating 0..15) holds the emission
+  // -|d|^2 of LUT entry k, d = c sk - w_t sk; two tables, for the step parities,
+  // fill the LUT's 16 KiB.  State s's emission sits at half the byte its codeword
+  // has in the LUT (plus 8 KiB for odd steps), and a wave's 64 reads fall in
+  // distinct banks (col_walk_unit).  The kernel runs 256 threads here; thread
+  // tid forms entries tid + 256j (j < 4) and their row copies, reading the
+  // codewords from the (2^Q, 2) table as stage_hyb_col does.
   // Column-walk bases of this thread's butterfly u = utid, input c (state R*u + c),
   // for the beta sweep; the alpha sweep forms its output's base as it goes.
   uint32_t cbs[kCol ? R : 1];
@@ -195,12 +196,12 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
       using Fast = std::integral_constant<bool, EXACT>;
 
       // ------------------------------ alpha sweep ------------------------------
-      // Emission table of step t into buffer t & 1 (kETab).
+      // Emission table of step t into table t & 1 (kETab).
       auto build_etab = [&](int t) {
         float nwt[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) nwt[v] = -wbuf[t * V + v] * sk;
-        float* et = lut + (t & 1);
+        float* et = lut + 2048 * (t & 1);
         const int ncol = 1 << (P.Q - 3), mask = (1 << P.Q) - 1;
         float h[4][2];
 #pragma unroll
@@ -219,8 +220,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
             e = fmaf(-d, d, e);
           }
           const int k = tid + 256 * j;
-          et[2 * k] = e;
-          et[2 * (k + 1024)] = e;
+          et[k] = e;
+          et[k + 1024] = e;
         }
       };
       if constexpr (kETab) {
@@ -242,10 +243,10 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         float nw[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) nw[v] = -wbuf[t * V + v] * sk;
-        // The next step's emission table goes to the buffer step t - 1 read,
-        // which every wave has left (barrier at the end of each step).
+        // The next step's emission table goes where step t - 1's was, which
+        // every wave has left (barrier at the end of each step).
         if (kETab && t + 1 < N) build_etab(t + 1);
-        const uint32_t eoff = 4u * (uint32_t)(t & 1);
+        const uint32_t eoff = 8192u * (uint32_t)(t & 1);
 
         // Output r of butterfly u (unit i) from the shifted inputs m[p]
         // (maximum 0): returns the group sum, mo = m~_t(R*u + r).
@@ -260,8 +261,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
             // The two-rounding d_3inst form is kept out of the low-temperature
             // variant, where |d| reaches ~1e2 and float32 precision is tightest.
             const bool cached = i < CU;
-            if constexpr (kETab) {
-              acc += *reinterpret_cast<const float*>(lutb + cb + hyb_col_step(p, r));
+            if constexpr (kETab) {  // cb: the table byte of state R*u + r's row 0 entry
+              acc += *reinterpret_cast<const float*>(lutb + cb + (hyb_col_step(p, r) >> 1));
             } else if (!cached && CODE == CODE_3INST && !EXACT) {
               const float d = d_3inst(xu + p * ANT + CT::A * (uint32_t)r, ssk, nw[0]);
               acc = fmaf(-d, d, acc);
@@ -355,7 +356,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
               for (int r = 0; r < R; ++r) {
                 float mo;
-                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, cbs[r] + eoff);
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, (cbs[r] >> 1) + eoff);
                 smin = r ? fminf(smin, s) : s;
                 cur[e16 ^ (uint32_t)r] = mo;
                 tmax = vmax_raw(tmax, mo);
@@ -366,7 +367,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
                   for (int r = 0; r < R; ++r) {
                     float mo;
                     alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo,
-                              hyb_col_base((uint32_t)(R * u + r), P.Q) + eoff);
+                              (hyb_col_base((uint32_t)(R * u + r), P.Q) >> 1) + eoff);
                     cur[e16 ^ (uint32_t)r] = mo;
                     tmax = vmax_raw(tmax, mo);
                   }

@@ -171,11 +171,13 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
       rbuf[NT + j] = (cons && ((uint32_t)j >> (L - KV - ob)) != ov) ? kVitInf : 0.0f;
     // Column walk: the cost E_t of every LUT entry, computed once per step as
     // the state loop would (same operations and order, so the same float), sits
-    // in the LUT copies' place: entry k's cost of step t is the float at the byte
-    // of its codeword's float2 in each copy, plus 4 (t & 1).  The LUT copies
-    // come back after the loop.
+    // in the LUT copies' place, one table per step parity (32 KiB each): entry
+    // k's cost of step t is float (k << kColRep | copy) of table t & 1, at half
+    // the byte of its codeword's float2 in the LUT copies, and a wave's reads fall
+    // in distinct banks.  The LUT copies come back after the loop.
+    static_assert(!kColV || kColRep == 2, "one float4 per table entry");
     auto build_cost = [&](int t) {
-      float* dst = reinterpret_cast<float*>(lut2) + (t & 1);
+      float4* dst = reinterpret_cast<float4*>(reinterpret_cast<float*>(lut2) + 8192 * (t & 1));
       for (int k = tid; k < 16 * 64; k += nthr) {
         const float2 cv = col_entry(k);
         const float d0 = cv.x - wbuf[t * V];
@@ -183,11 +185,8 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
         float e = 0.0f;
         e = e + d0 * d0;
         e = e + d1 * d1;
-#pragma unroll
-        for (int cp = 0; cp < (1 << kColRep); ++cp) {
-          dst[2 * ((k << kColRep) | cp)] = e;
-          dst[2 * (((k + 16 * 64) << kColRep) | cp)] = e;
-        }
+        dst[k] = make_float4(e, e, e, e);  // the four copies
+        dst[k + 16 * 64] = make_float4(e, e, e, e);
       }
     };
     if constexpr (kColV) build_cost(0);
@@ -199,10 +198,10 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
       float w[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) w[v] = wbuf[t * V + v];
-      // the next step's table goes to the buffer step t - 1 read (every wave
-      // has left it: barrier at the end of each step)
+      // the next step's table goes where step t - 1's was (every wave has left
+      // it: barrier at the end of each step)
       if (kColV && t + 1 < N) build_cost(t + 1);
-      const uint32_t eoff = 4u * (uint32_t)(t & 1);
+      const uint32_t eoff = 32768u * (uint32_t)(t & 1);
 #pragma unroll
       for (int i = 0; i < UPT; ++i) {
         const int q = tid + i * nthr;
@@ -215,39 +214,51 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
           for (int p = 0; p < R; ++p) ri[p] = prev[p * NB + u];
           float ro[RO];
           uint32_t bpw = 0;
+          // The column walk's row step of output sub4 + r depends on it mod 8
+          // (hyb_col_step), so each wave takes one of two unrolled copies
+          // (sub4 mod 8 = SO, 0 or 4) whose cost reads are base + immediate.
+          auto outputs = [&](auto so_tag) {
+            constexpr int SO = decltype(so_tag)::value;
 #pragma unroll
-          for (int r = 0; r < RO; ++r) {
-            const int rr = sub * RO + r;
-            float best = 0.0f;
-            int bi = 0;
+            for (int r = 0; r < RO; ++r) {
+              const int rr = sub * RO + r;
+              float best = 0.0f;
+              int bi = 0;
+              const uint32_t ebase = kColV ? (cbv[r] >> 1) + eoff : 0u;  // table byte of output r's row-0 entry
 #pragma unroll
-            for (int p = 0; p < R; ++p) {
-              float c[V];
-              float e = 0.0f;
-              if constexpr (kColV) {
-                e = *reinterpret_cast<const float*>(lutb + cbv[r] + (hyb_col_step(p, sub4 + r) << kColRep) + eoff);
-              } else {
-                if constexpr (CACHE) {
-#pragma unroll
-                  for (int v = 0; v < V; ++v) c[v] = cw[i][p][r][v];
+              for (int p = 0; p < R; ++p) {
+                float c[V];
+                float e = 0.0f;
+                if constexpr (kColV) {
+                  e = *reinterpret_cast<const float*>(lutb + ebase + (hyb_col_step(p, SO + r) << (kColRep - 1)));
                 } else {
-                  cword((uint32_t)(p * NT + R * u + rr), c);
-                }
+                  if constexpr (CACHE) {
 #pragma unroll
-                for (int v = 0; v < V; ++v) {
-                  const float d = c[v] - w[v];
-                  const float d2 = d * d;
-                  e = e + d2;
+                    for (int v = 0; v < V; ++v) c[v] = cw[i][p][r][v];
+                  } else {
+                    cword((uint32_t)(p * NT + R * u + rr), c);
+                  }
+#pragma unroll
+                  for (int v = 0; v < V; ++v) {
+                    const float d = c[v] - w[v];
+                    const float d2 = d * d;
+                    e = e + d2;
+                  }
+                }
+                const float cum = ri[p] + e;
+                if (p == 0 || cum < best) {
+                  best = cum;
+                  bi = p;
                 }
               }
-              const float cum = ri[p] + e;
-              if (p == 0 || cum < best) {
-                best = cum;
-                bi = p;
-              }
+              ro[r] = best;
+              bpw |= (uint32_t)bi << (8 * r);
             }
-            ro[r] = best;
-            bpw |= (uint32_t)bi << (8 * r);
+          };
+          if (kColV && (sub4 & 4)) {
+            outputs(std::integral_constant<int, 4>{});
+          } else {
+            outputs(std::integral_constant<int, 0>{});
           }
           store_vec<RO>(cur + R * u + sub * RO, ro);
           if constexpr (PACK) {  // entries R*u + sub*RO .. +RO-1 at kV bits each

@@ -271,15 +271,18 @@ def test_column_walk_layouts_are_bank_conflict_free():
     half-wave from 32 eight-byte banks, 64-bit writes each quarter-wave from 32
     four-byte banks, 32-bit reads 64 lanes from 64 banks, 32-bit writes 32 lanes
     from 32 banks.  Checked: the LUT gathers at Q = 9 (bank = bits [6, 11) of
-    r^2 + r, r = 16u + c), the forward's alpha and beta state layouts, and the
-    backward's swizzled (m~, mu) pairs at the rotations 0, 4, 8."""
+    r^2 + r, r = 16u + c), the 32-bit reads of the per-step emission tables in
+    the LUT's layout (bank = bits [6, 12)), the forward's alpha and beta state
+    layouts, and the backward's swizzled (m~, mu) pairs at the rotations 0, 4, 8."""
     M = _col_walk_maps()
     tid = np.arange(256, dtype=np.int64)
     U = M["col_walk_unit"](tid)
     assert sorted(U.tolist()) == list(range(256))
     lut_bank = lambda r: ((r * r + r) >> 6) & 31
+    table_bank = lambda r: ((r * r + r) >> 6) & 63
     for c in range(16):
         assert _distinct_in_groups(lut_bank(16 * U + c), 32, 32), c
+        assert _distinct_in_groups(table_bank(16 * U + c), 64, 64), c
     # the lane map is what makes the gathers conflict-free: u = tid collides
     assert not _distinct_in_groups(lut_bank(16 * tid), 32, 32)
 
