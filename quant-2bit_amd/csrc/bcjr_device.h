@@ -134,15 +134,14 @@ __host__ __device__ constexpr uint32_t col_walk_unit(uint32_t tid) {
   return ((tid >> 6) & 3u) | ((tid & 63u) << 2);
 }
 
-// LDS layouts of the column-walk forward's reduced state j (12 bits, element
-// E(j)), conflict-free under col_walk_unit for the accesses of each sweep:
-// alpha reads j = 256p + u (one per p, 64 lanes, 4-byte banks mod 64) and writes
-// j = 16u + r (half-waves, mod 32); beta reads j = 16u + c (mod 64) and writes
-// j = 256p + u (mod 32).  Both are linear bijections with E(c) = c for c < 16,
-// so E(16u + c) = E(16u) ^ c and E(256p + u) = 256p + (E(u) ^ E(256p) mod 256).
-__host__ __device__ constexpr uint32_t col_walk_alpha_el(uint32_t j) { return j ^ ((j >> 6) & 31u); }
-__host__ __device__ constexpr uint32_t col_walk_beta_el(uint32_t j) {
-  return j ^ ((j >> 4) & 3u) ^ ((j >> 6) & 63u);
+// LDS layout of the column-walk forward's one state vector: with the rotation of
+// step t applied, x = rotr(j, rho_t), reduced state j sits at element
+// col_walk_state_el(x).  Under col_walk_unit, every 32-bit read (64 lanes, banks
+// mod 64) and write (32 lanes, mod 32) of x = rotr(k*256 + u, rho) is
+// conflict-free, for k < 16 and rho = 0, 4, 8.  Linear, so the element of
+// k*256 + u is that of u XOR that of k*256.
+__host__ __device__ constexpr uint32_t col_walk_state_el(uint32_t x) {
+  return x ^ ((x >> 4) & 3u) ^ ((x >> 6) & 63u) ^ ((x >> 7) & 31u);
 }
 
 // Any state from the column-walk LUT (rows 0..15).

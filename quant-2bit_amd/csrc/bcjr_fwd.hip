@@ -54,7 +54,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   static_assert(!kCol || (KV == 4 && UPT == 1), "the column walk is for L = 16, kV = 4");
   // Its outputs are unrolled except in the diagnostics instance, which would spill.
   constexpr bool kColUnroll = kCol && !INTERNALS;
-  // Its alpha sweep reads each state's emission from a per-step table (below).
+  // Its sweeps read each state's emission (and, in the beta sweep, codeword)
+  // from a per-step table, and keep one state vector, updated in place (below).
   constexpr bool kETab = kColUnroll;
   using CT = CodeTraits<CODE>;
 
@@ -66,13 +67,20 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
   // The column-walk instance gives thread tid butterfly col_walk_unit(tid), so
-  // that its LUT and emission-table reads hit distinct banks, and lays its alpha and beta
-  // state vectors out by col_walk_alpha_el / col_walk_beta_el; elsewhere u = tid.
+  // that its table reads hit distinct banks; elsewhere u = tid.
   const int utid = kColUnroll ? (int)col_walk_unit((uint32_t)tid) : tid;
+  // kETab: the one state vector is updated in place.  At step t (either sweep)
+  // butterfly u reads and writes the elements st_el(k*NB + u, rho_t), k < R,
+  // rho_t = kV (t - 1) mod nb: rotr(R*u + r, kV) = r*NB + u, so its outputs land
+  // on its inputs, and col_walk_state_el keeps every access conflict-free.
+  const int nbits = L - KV;
+  auto st_el = [&](uint32_t j, int rho) -> uint32_t { return col_walk_state_el(rotr_bits(j, rho, nbits)); };
 
   double* cvec = reinterpret_cast<double*>(smem);                // N    C_{t-1}
-  float* mbuf = reinterpret_cast<float*>(cvec + ((N + 1) & ~1));  // 2*NT reduced state (16-B aligned)
-  float* wmax = mbuf + 2 * NT;                                    // 2*kMaxWaves
+  // Reduced state (16-B aligned): 2*NT floats, double-buffered by step; kETab:
+  // NT floats, then the 32 KiB table region.
+  float* mbuf = reinterpret_cast<float*>(cvec + ((N + 1) & ~1));
+  float* wmax = mbuf + (kETab ? NT + 8192 : 2 * NT);              // 2*kMaxWaves
   float* wsum = wmax + 2 * kMaxWaves;                             // kMaxWaves
   // Last wsum word: the block-wide input flag (at most 8 waves use wsum, launch
   // bounds 512 threads), 0 outside the check at the start of each sequence.
@@ -82,8 +90,11 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   // diagnostics variant, of sum_s P log2 P (one more), double-buffered by step.
   constexpr int SP = V + 1;
   float* spart = wbuf + N * V;                                    // 2*nwaves*SP per-wave partials
-  // HYB: signed LUT (code_hyb_signed) or column-walk LUT (hyb_col_base), 8-byte aligned
-  float* lut = reinterpret_cast<float*>(smem) + ((spart + 2 * nwaves * SP - reinterpret_cast<float*>(smem) + 1) & ~1);
+  // HYB: signed LUT (code_hyb_signed) or column-walk LUT (hyb_col_base), 8-byte
+  // aligned; kETab: the per-step tables after the state vector, 16-byte aligned.
+  float* lut = kETab ? mbuf + NT
+                     : reinterpret_cast<float*>(smem) +
+                           ((spart + 2 * nwaves * SP - reinterpret_cast<float*>(smem) + 1) & ~1);
 
   if constexpr (CODE == CODE_HYB) {
     stage_hyb_signed(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
@@ -93,21 +104,29 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
     __syncthreads();
   }
   const unsigned char* lutb = reinterpret_cast<const unsigned char*>(lut);
-  // Emission table of the column-walk alpha sweep, in the LUT's place until the
-  // beta sweep stages the LUT: per step, float k of the table (the column-walk
-  // layout: 32 rows of 64, rows 16..31 repeating 0..15) holds the emission
-  // -|d|^2 of LUT entry k, d = c sk - w_t sk; two tables, for the step parities,
-  // fill the LUT's 16 KiB.  State s's emission sits at half the byte its codeword
-  // has in the LUT (plus 8 KiB for odd steps), and a wave's 64 reads fall in
-  // distinct banks (col_walk_unit).  The kernel runs 256 threads here; thread
-  // tid forms entries tid + 256j (j < 4) and their row copies, reading the
-  // codewords from the (2^Q, 2) table as stage_hyb_col does.
-  // Column-walk bases of this thread's butterfly u = utid, input c (state R*u + c),
-  // for the beta sweep; the alpha sweep forms its output's base as it goes.
+  // Per-step tables of the column walk, in the 32 KiB region.  Alpha sweep:
+  // float k of the table (the column-walk layout: 32 rows of 64, rows 16..31
+  // repeating 0..15) holds the emission -|d|^2 of LUT entry k, d = c sk - w_t sk;
+  // two tables, for the step parities, take 16 KiB.  State s's emission sits at
+  // a quarter of the byte its codeword would have in a float4 table (plus 8 KiB
+  // for odd steps), and a wave's 64 reads fall in distinct banks (col_walk_unit).
+  // Beta sweep: one float4 table, entry k = (-|d|^2, c) of LUT entry k, rebuilt
+  // per step behind a barrier.  The kernel runs 256 threads here; thread tid
+  // forms entries tid + 256j (j < 4) and their row copies, reading the codewords
+  // from the (2^Q, 2) table as stage_hyb_col does.
+  auto col_codeword = [&](int kk, float& h0, float& h1) {
+    const int ncol = 1 << (P.Q - 3), mask = (1 << P.Q) - 1;
+    const int col = kk & 63, ii = col + ncol * (kk >> 6), ie = ii & mask;
+    h0 = col < ncol ? P.table[2 * ie] : 0.0f;
+    const float y = col < ncol ? P.table[2 * ie + 1] : 0.0f;
+    h1 = (ii >> P.Q) ? -y : y;
+  };
+  // Column-walk bases of this thread's butterfly u = utid, input c (state R*u + c)
+  // (kETab: doubled, the float4 table's byte of the row 0 entry).
   uint32_t cbs[kCol ? R : 1];
   if constexpr (kCol) {
 #pragma unroll
-    for (int c = 0; c < R; ++c) cbs[c] = hyb_col_base((uint32_t)(R * min(utid, NB - 1) + c), P.Q);
+    for (int c = 0; c < R; ++c) cbs[c] = hyb_col_base((uint32_t)(R * min(utid, NB - 1) + c), P.Q) << (kETab ? 1 : 0);
   }
 
   // Raw codewords h of this thread's first CU butterflies, fixed for the
@@ -162,7 +181,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
       bad |= !__builtin_isfinite(w);
     }
     // m~_{-1} = log2(R) everywhere: the buffer step 0 reads from.
-    for (int j = tid; j < NT; j += nthr) mbuf[NT + j] = (float)KV;
+    for (int j = tid; j < NT; j += nthr) mbuf[(kETab ? 0 : NT) + j] = (float)KV;
     if (tid < 2 * kMaxWaves) wmax[tid] = -INFINITY;  // waves that do not exist
     if (bad) *bflag = 1;
     __syncthreads();
@@ -202,15 +221,9 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
         for (int v = 0; v < V; ++v) nwt[v] = -wbuf[t * V + v] * sk;
         float* et = lut + 2048 * (t & 1);
-        const int ncol = 1 << (P.Q - 3), mask = (1 << P.Q) - 1;
         float h[4][2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int k = tid + 256 * j, col = k & 63, i = col + ncol * (k >> 6), ie = i & mask;
-          h[j][0] = col < ncol ? P.table[2 * ie] : 0.0f;
-          const float y = col < ncol ? P.table[2 * ie + 1] : 0.0f;
-          h[j][1] = (i >> P.Q) ? -y : y;
-        }
+        for (int j = 0; j < 4; ++j) col_codeword(tid + 256 * j, h[j][0], h[j][1]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           float e = 0.0f;
@@ -230,9 +243,17 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
       }
       double C = 0.0;  // C_{t-1}
       int k = 0;       // step counter across both sweeps: LDS buffer / wmax parity
+      int rho = nbits - KV;  // kV (t - 1) mod nb at t = 0 (kETab)
       for (int t = 0; t < N; ++t, ++k) {
-        const float* prev = mbuf + ((k + 1) & 1) * NT;
-        float* cur = mbuf + (k & 1) * NT;
+        const float* prev = mbuf + (kETab ? 0 : ((k + 1) & 1) * NT);
+        float* cur = mbuf + (kETab ? 0 : (k & 1) * NT);
+        // kETab: element st_el(k*NB + u, rho) = ebase ^ Kel[k] of butterfly u = utid
+        const uint32_t ebase = kETab ? st_el((uint32_t)utid, rho) : 0u;
+        uint32_t Kel[kETab ? R : 1];
+        if constexpr (kETab) {
+#pragma unroll
+          for (int q = 0; q < R; ++q) Kel[q] = st_el((uint32_t)(q * NB), rho);
+        }
         float O = (float)KV;  // m~_{-1} = log2(R) for every j
         if (t > 0) {
           O = -INFINITY;
@@ -299,16 +320,13 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         };
 
         // Inputs of butterfly utid + i*nthr; the next butterfly's are read
-        // before the current one's arithmetic (prev is read-only this step).
-        // The column-walk instance keeps the reduced alpha state j at element
-        // col_walk_alpha_el(j), whose low six bits for j = p*NB + u (NB = 256)
-        // are those of E(u) ^ E(256p).
+        // before the current one's arithmetic (prev is read-only this step; in
+        // place, a thread's elements are its own).
         auto read_in = [&](int i, float (&m)[R]) {
           const int qq = min(utid + i * nthr, NB - 1);
-          if constexpr (kColUnroll) {
-            const uint32_t eu = col_walk_alpha_el((uint32_t)qq);
+          if constexpr (kETab) {
 #pragma unroll
-            for (int p = 0; p < R; ++p) m[p] = prev[p * NB + (eu ^ (col_walk_alpha_el((uint32_t)p << 8) & 255u))];
+            for (int p = 0; p < R; ++p) m[p] = prev[ebase ^ Kel[p]];
           } else {
 #pragma unroll
             for (int p = 0; p < R; ++p) m[p] = prev[p * NB + qq];
@@ -352,13 +370,12 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
               // Outputs unrolled, so every state's LUT offset is an immediate;
               // a butterfly with an underflowed group is redone output by output.
               float smin = 0.0f;
-              const uint32_t e16 = col_walk_alpha_el((uint32_t)(R * u));  // element of state R*u + r: e16 ^ r
 #pragma unroll
               for (int r = 0; r < R; ++r) {
                 float mo;
-                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, (cbs[r] >> 1) + eoff);
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, oout, mo, (cbs[r] >> 2) + eoff);
                 smin = r ? fminf(smin, s) : s;
-                cur[e16 ^ (uint32_t)r] = mo;
+                cur[ebase ^ Kel[r]] = mo;
                 tmax = vmax_raw(tmax, mo);
               }
               if constexpr (!EXACT) {
@@ -368,7 +385,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
                     float mo;
                     alpha_out(std::true_type{}, i, r, xu, u, m, oout, mo,
                               (hyb_col_base((uint32_t)(R * u + r), P.Q) >> 1) + eoff);
-                    cur[e16 ^ (uint32_t)r] = mo;
+                    cur[ebase ^ Kel[r]] = mo;
                     tmax = vmax_raw(tmax, mo);
                   }
                 }
@@ -388,16 +405,12 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         }
         tmax = wave_max(tmax);
         if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
+        rho = rho + KV >= nbits ? rho + KV - nbits : rho + KV;
         __syncthreads();
       }
 
-      // The beta sweep reads codewords: the LUT replaces the emission table
-      // (every wave has left the table at the last alpha step's barrier; the
-      // barriers below come before the first LUT read).
-      if constexpr (kETab) stage_hyb_col(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
-
       // log2 Z = C_{N-1} + LSE2 over the final reduced state.
-      const float* fin = mbuf + ((k + 1) & 1) * NT;
+      const float* fin = mbuf + (kETab ? 0 : ((k + 1) & 1) * NT);
       float Mz = -INFINITY;
       Mz = block_max(wmax + ((k + 1) & 1) * kMaxWaves);
       float part = 0.0f;
@@ -409,7 +422,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
       for (int w = 0; w < nwaves; ++w) Ssum += wsum[w];
       logZ2 = C + (double)Mz + (double)flog2(Ssum);
       // n~_{N-1} = 0: the buffer step N-1 of the beta sweep reads from.
-      for (int j = tid; j < NT; j += nthr) mbuf[((k + 1) & 1) * NT + j] = 0.0f;
+      for (int j = tid; j < NT; j += nthr) mbuf[(kETab ? 0 : ((k + 1) & 1) * NT) + j] = 0.0f;
       __syncthreads();
 
       // ------------------------------ beta sweep -------------------------------
@@ -426,9 +439,17 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         if (UPT > 1 || N > 1) load_vec<R>(UPT > 1 ? slot_src(N - 1, 1) : slot_src(N - 2, 0), pb);
       }
       double D = 0.0;  // D_t
+      // rho_t = kV * (t - 1) mod nb at t = N - 1 (kETab)
+      rho = (int)(((long long)KV * (N - 2) % nbits + nbits) % nbits);
       for (int t = N - 1; t >= 0; --t, ++k) {
-        const float* prev = mbuf + ((k + 1) & 1) * NT;
-        float* cur = mbuf + (k & 1) * NT;
+        const float* prev = mbuf + (kETab ? 0 : ((k + 1) & 1) * NT);
+        float* cur = mbuf + (kETab ? 0 : (k & 1) * NT);
+        const uint32_t ebase = kETab ? st_el((uint32_t)utid, rho) : 0u;
+        uint32_t Kel[kETab ? R : 1];
+        if constexpr (kETab) {
+#pragma unroll
+          for (int q = 0; q < R; ++q) Kel[q] = st_el((uint32_t)(q * NB), rho);
+        }
         float Qv = 0.0f;
         if (t != N - 1) {
           Qv = -INFINITY;
@@ -440,6 +461,21 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         float nw[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) nw[v] = -wbuf[t * V + v] * sk;
+        if constexpr (kETab) {  // every wave has left step t+1's table (barrier at its end)
+          float4* et = reinterpret_cast<float4*>(lut);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int kk = tid + 256 * j;
+            float h0, h1;
+            col_codeword(kk, h0, h1);
+            const float d0 = fmaf(h0, ssk, nw[0]);
+            const float d1 = fmaf(h1, ssk, nw[1]);
+            const float e = fmaf(-d1, d1, fmaf(-d0, d0, 0.0f));
+            et[kk] = make_float4(e, h0, h1, 0.0f);
+            et[kk + 1024] = make_float4(e, h0, h1, 0.0f);
+          }
+          __syncthreads();
+        }
 
         // Output p of butterfly u (unit i) from the shifted inputs nr[c]
         // (maximum 0): no = n~_{t-1}(p*NB + u) and the soft contribution
@@ -453,6 +489,13 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           float y[R], hh[R][V];
 #pragma unroll
           for (int c = 0; c < R; ++c) {
+            if constexpr (kETab) {
+              const float4 eh = *reinterpret_cast<const float4*>(lutb + cbs[c] + 2 * hyb_col_step(p, c));
+              y[c] = nr[c] + eh.x;
+              hh[c][0] = eh.y;
+              hh[c][1] = eh.z;
+              continue;
+            }
             if (i < CU) {
 #pragma unroll
               for (int v = 0; v < V; ++v) hh[c][v] = hc[i < CU ? i : 0][p][c][v];
@@ -511,13 +554,11 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           return s;
         };
 
-        // The column-walk instance reads state R*u + c at col_walk_beta_el(R*u) ^ c.
         auto read_in = [&](int i, float (&n)[R]) {
           const int qq = min(utid + i * nthr, NB - 1);
-          if constexpr (kColUnroll) {
-            const uint32_t f16 = col_walk_beta_el((uint32_t)(R * qq));
+          if constexpr (kETab) {
 #pragma unroll
-            for (int c = 0; c < R; ++c) n[c] = prev[f16 ^ (uint32_t)c];
+            for (int c = 0; c < R; ++c) n[c] = prev[ebase ^ Kel[c]];
           } else {
             load_vec<R>(prev + R * qq, n);
           }
@@ -596,8 +637,6 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
               // Outputs unrolled, so every state's LUT offset is an immediate;
               // the butterfly's sums are redone when a group underflowed.
               const float* src = slot_src(t, i);
-              // element of state p*NB + u: p*NB + (fu ^ low bits of E(256p))
-              const uint32_t fu = col_walk_beta_el((uint32_t)u);
               float smin = 0.0f, ua[V], uh = 0.0f;
 #pragma unroll
               for (int v = 0; v < V; ++v) ua[v] = 0.0f;
@@ -610,7 +649,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
                 for (int v = 0; v < V; ++v) ua[v] += cs[v];
                 uh += hs;
-                cur[p * NB + (fu ^ (col_walk_beta_el((uint32_t)p << 8) & 255u))] = no;
+                cur[ebase ^ Kel[p]] = no;
                 tmax = vmax_raw(tmax, no);
               }
               if constexpr (!EXACT) {
@@ -626,7 +665,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
                     for (int v = 0; v < V; ++v) ua[v] += cs[v];
                     uh += hs;
-                    cur[p * NB + (fu ^ (col_walk_beta_el((uint32_t)p << 8) & 255u))] = no;
+                    cur[ebase ^ Kel[p]] = no;
                     tmax = vmax_raw(tmax, no);
                   }
                 }
@@ -664,6 +703,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         }
         tmax = wave_max(tmax);
         if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
+        rho = rho - KV < 0 ? rho - KV + nbits : rho - KV;
         __syncthreads();
       }
     };

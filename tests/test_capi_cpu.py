@@ -246,7 +246,7 @@ def _col_walk_maps():
     csrc = os.path.join(ROOT, "quant-2bit_amd", "csrc")
     dev = open(os.path.join(csrc, "bcjr_device.h")).read()
     maps = {}
-    for name in ("col_walk_unit", "col_walk_alpha_el", "col_walk_beta_el"):
+    for name in ("col_walk_unit", "col_walk_state_el"):
         m = re.search(name + r"\(uint32_t (\w+)\) \{\s*return ([^;]+);", dev)
         assert m, name
         body = re.sub(r"(\d+)u\b", r"\1", m.group(2))
@@ -272,8 +272,9 @@ def test_column_walk_layouts_are_bank_conflict_free():
     four-byte banks, 32-bit reads 64 lanes from 64 banks, 32-bit writes 32 lanes
     from 32 banks.  Checked: the LUT gathers at Q = 9 (bank = bits [6, 11) of
     r^2 + r, r = 16u + c), the 32-bit reads of the per-step emission tables in
-    the LUT's layout (bank = bits [6, 12)), the forward's alpha and beta state
-    layouts, and the backward's swizzled (m~, mu) pairs at the rotations 0, 4, 8."""
+    the LUT's layout (bank = bits [6, 12)), and the in-place state vectors at the
+    rotations 0, 4, 8: the forward's floats (col_walk_state_el, 32-bit) and the
+    backward's swizzled (m~, mu) pairs (64-bit)."""
     M = _col_walk_maps()
     tid = np.arange(256, dtype=np.int64)
     U = M["col_walk_unit"](tid)
@@ -287,26 +288,21 @@ def test_column_walk_layouts_are_bank_conflict_free():
     assert not _distinct_in_groups(lut_bank(16 * tid), 32, 32)
 
     j = np.arange(4096, dtype=np.int64)
-    for name, reads, writes in (("col_walk_alpha_el", "256p+u", "16u+c"), ("col_walk_beta_el", "16u+c", "256p+u")):
-        E = M[name]
-        assert sorted(E(j).tolist()) == list(range(4096)), name
-        assert np.array_equal(E(np.arange(16)), np.arange(16)), name
-        for p in range(16):  # the split the kernels address with
-            assert np.array_equal(E(256 * p + U), 256 * p + ((E(U) ^ E(256 * p)) & 255)), name
-            assert np.array_equal(E(16 * U + p), E(16 * U) ^ p), name
-        acc = {"256p+u": [256 * p + U for p in range(16)], "16u+c": [16 * U + c for c in range(16)]}
-        for idx in acc[reads]:
-            assert _distinct_in_groups(E(idx), 64, 64), (name, "read")
-        for idx in acc[writes]:
-            assert _distinct_in_groups(E(idx), 32, 32), (name, "write")
-
-    S = M["swizzle"]
-    assert sorted(S(j).tolist()) == list(range(4096))
     rotr = lambda x, rho: ((x | (x << 12)) >> rho) & 4095
+    # in place: butterfly u's outputs 16u + r of one step are its inputs r*256 + u
+    # of the next, one rotation by kV = 4 later
+    for r in range(16):
+        assert np.array_equal(rotr(16 * U + r, 4), 256 * r + U)
+    E, S = M["col_walk_state_el"], M["swizzle"]
+    for layout in (E, S):
+        assert sorted(layout(j).tolist()) == list(range(4096))
     for rho in (0, 4, 8):
         for k in range(16):
-            el = S(rotr(256 * k + U, rho))
-            assert _distinct_in_groups(el, 32, 32) and _distinct_in_groups(el, 16, 16), (rho, k)
+            x = rotr(256 * k + U, rho)
+            # the split the forward addresses with: element of u XOR element of k*256
+            assert np.array_equal(E(x), E(rotr(U, rho)) ^ E(rotr(np.full_like(U, 256 * k), rho)))
+            assert _distinct_in_groups(E(x), 64, 64) and _distinct_in_groups(E(x), 32, 32), (rho, k)
+            assert _distinct_in_groups(S(x), 32, 32) and _distinct_in_groups(S(x), 16, 16), (rho, k)
 
 
 # ------------------------- contract checks (no device) -------------------------
