@@ -104,16 +104,20 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
     __syncthreads();
   }
   const unsigned char* lutb = reinterpret_cast<const unsigned char*>(lut);
+  float2* hcomp = reinterpret_cast<float2*>(lut + 4096);  // kETab, alpha sweep
   // Per-step tables of the column walk, in the 32 KiB region.  Alpha sweep:
   // float k of the table (the column-walk layout: 32 rows of 64, rows 16..31
   // repeating 0..15) holds the emission -|d|^2 of LUT entry k, d = c sk - w_t sk;
   // two tables, for the step parities, take 16 KiB.  State s's emission sits at
   // a quarter of the byte its codeword would have in a float4 table (plus 8 KiB
   // for odd steps), and a wave's 64 reads fall in distinct banks (col_walk_unit).
-  // Beta sweep: one float4 table, entry k = (-|d|^2, c) of LUT entry k, rebuilt
-  // per step behind a barrier.  The kernel runs 256 threads here; thread tid
-  // forms entries tid + 256j (j < 4) and their row copies, reading the codewords
-  // from the (2^Q, 2) table as stage_hyb_col does.
+  // Beta sweep: one float4 table, entry k = (c, -|d|^2, 0) of LUT entry k, whose
+  // emissions are rewritten per step behind a barrier.  The kernel runs 256
+  // threads here; thread tid forms entries tid + 256j (j < 4) and their row
+  // copies.  The codewords come from the LDS: during the alpha sweep from a
+  // float2 copy of LUT entries 0..1023 in the region's second half (hcomp,
+  // filled per sequence from the (2^Q, 2) table as stage_hyb_col forms them),
+  // during the beta sweep from the float4 table itself.
   auto col_codeword = [&](int kk, float& h0, float& h1) {
     const int ncol = 1 << (P.Q - 3), mask = (1 << P.Q) - 1;
     const int col = kk & 63, ii = col + ncol * (kk >> 6), ie = ii & mask;
@@ -182,6 +186,14 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
     }
     // m~_{-1} = log2(R) everywhere: the buffer step 0 reads from.
     for (int j = tid; j < NT; j += nthr) mbuf[(kETab ? 0 : NT) + j] = (float)KV;
+    if constexpr (kETab) {  // the previous sequence's last barrier ended every table read
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float h0, h1;
+        col_codeword(tid + 256 * j, h0, h1);
+        hcomp[tid + 256 * j] = make_float2(h0, h1);
+      }
+    }
     if (tid < 2 * kMaxWaves) wmax[tid] = -INFINITY;  // waves that do not exist
     if (bad) *bflag = 1;
     __syncthreads();
@@ -221,17 +233,12 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
         for (int v = 0; v < V; ++v) nwt[v] = -wbuf[t * V + v] * sk;
         float* et = lut + 2048 * (t & 1);
-        float h[4][2];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) col_codeword(tid + 256 * j, h[j][0], h[j][1]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          float e = 0.0f;
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            const float d = fmaf(h[j][v], ssk, nwt[v]);
-            e = fmaf(-d, d, e);
-          }
+          const float2 h = hcomp[tid + 256 * j];
+          const float d0 = fmaf(h.x, ssk, nwt[0]);
+          const float d1 = fmaf(h.y, ssk, nwt[1]);
+          const float e = fmaf(-d1, d1, fmaf(-d0, d0, 0.0f));
           const int k = tid + 256 * j;
           et[k] = e;
           et[k + 1024] = e;
@@ -409,6 +416,13 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         __syncthreads();
       }
 
+      // kETab: this thread's codewords, before the float4 table overwrites hcomp
+      float2 hv[kETab ? 4 : 1];
+      if constexpr (kETab) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hv[j] = hcomp[tid + 256 * j];
+      }
+
       // log2 Z = C_{N-1} + LSE2 over the final reduced state.
       const float* fin = mbuf + (kETab ? 0 : ((k + 1) & 1) * NT);
       float Mz = -INFINITY;
@@ -423,6 +437,15 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
       logZ2 = C + (double)Mz + (double)flog2(Ssum);
       // n~_{N-1} = 0: the buffer step N-1 of the beta sweep reads from.
       for (int j = tid; j < NT; j += nthr) mbuf[(kETab ? 0 : ((k + 1) & 1) * NT) + j] = 0.0f;
+      if constexpr (kETab) {  // codewords of the float4 table (every wave read hcomp before the barrier above)
+        float4* et = reinterpret_cast<float4*>(lut);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int kk = tid + 256 * j;
+          et[kk] = make_float4(hv[j].x, hv[j].y, 0.0f, 0.0f);
+          et[kk + 1024] = make_float4(hv[j].x, hv[j].y, 0.0f, 0.0f);
+        }
+      }
       __syncthreads();
 
       // ------------------------------ beta sweep -------------------------------
@@ -466,13 +489,12 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int kk = tid + 256 * j;
-            float h0, h1;
-            col_codeword(kk, h0, h1);
-            const float d0 = fmaf(h0, ssk, nw[0]);
-            const float d1 = fmaf(h1, ssk, nw[1]);
+            const float2 h = *reinterpret_cast<const float2*>(&et[kk]);
+            const float d0 = fmaf(h.x, ssk, nw[0]);
+            const float d1 = fmaf(h.y, ssk, nw[1]);
             const float e = fmaf(-d1, d1, fmaf(-d0, d0, 0.0f));
-            et[kk] = make_float4(e, h0, h1, 0.0f);
-            et[kk + 1024] = make_float4(e, h0, h1, 0.0f);
+            et[kk].z = e;
+            et[kk + 1024].z = e;
           }
           __syncthreads();
         }
@@ -490,10 +512,10 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll
           for (int c = 0; c < R; ++c) {
             if constexpr (kETab) {
-              const float4 eh = *reinterpret_cast<const float4*>(lutb + cbs[c] + 2 * hyb_col_step(p, c));
-              y[c] = nr[c] + eh.x;
-              hh[c][0] = eh.y;
-              hh[c][1] = eh.z;
+              const float4 he = *reinterpret_cast<const float4*>(lutb + cbs[c] + 2 * hyb_col_step(p, c));
+              y[c] = nr[c] + he.z;
+              hh[c][0] = he.x;
+              hh[c][1] = he.y;
               continue;
             }
             if (i < CU) {
