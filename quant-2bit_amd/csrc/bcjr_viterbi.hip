@@ -155,6 +155,10 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
       cbv[r] = (hyb_col_base((uint32_t)(R * (q0 & (NB - 1)) + sub4 + r), P.Q) << kColRep) + (copy << 3);
   }
 
+  // Column walk: the LUT entry whose cost this thread forms each step (entry tid;
+  // the instance runs 1024 threads), held for the launch.
+  const float2 cv_own = kColV ? col_entry(min(tid, 16 * 64 - 1)) : make_float2(0.0f, 0.0f);
+
   const int row_bytes = PACK ? (NT * KV) >> 3 : NT;  // backpointer bytes per step
   for (long long b = blockIdx.x; b < P.B; b += gridDim.x) {
     uint8_t* bp = P.ws + (size_t)blockIdx.x * (size_t)N * (size_t)NT;
@@ -175,22 +179,24 @@ __global__ __launch_bounds__(MAXT) void bcjr_viterbi_kernel(VitParams P) {
     // k's cost of step t is float (k << kColRep | copy) of table t & 1, at half
     // the byte of its codeword's float2 in the LUT copies, and a wave's reads fall
     // in distinct banks.  The LUT copies come back after the loop.
-    static_assert(!kColV || kColRep == 2, "one float4 per table entry");
+    static_assert(!kColV || (kColRep == 2 && MAXT == 1024), "one float4 per table entry, one entry per thread");
     auto build_cost = [&](int t) {
       float4* dst = reinterpret_cast<float4*>(reinterpret_cast<float*>(lut2) + 8192 * (t & 1));
-      for (int k = tid; k < 16 * 64; k += nthr) {
-        const float2 cv = col_entry(k);
-        const float d0 = cv.x - wbuf[t * V];
-        const float d1 = cv.y - wbuf[t * V + 1];
+      if (tid < 16 * 64) {  // entry tid
+        const float d0 = cv_own.x - wbuf[t * V];
+        const float d1 = cv_own.y - wbuf[t * V + 1];
         float e = 0.0f;
         e = e + d0 * d0;
         e = e + d1 * d1;
-        dst[k] = make_float4(e, e, e, e);  // the four copies
-        dst[k + 16 * 64] = make_float4(e, e, e, e);
+        dst[tid] = make_float4(e, e, e, e);  // the four copies
+        dst[tid + 16 * 64] = make_float4(e, e, e, e);
       }
     };
-    if constexpr (kColV) build_cost(0);
     __syncthreads();
+    if constexpr (kColV) {  // step 0's table, from the weights the barrier above published
+      build_cost(0);
+      __syncthreads();
+    }
 
     for (int t = 0; t < N; ++t) {
       const float* prev = rbuf + ((t + 1) & 1) * NT;
