@@ -129,9 +129,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   // codeword has in the LUT.  The kernel runs 256 threads here; thread tid forms
   // entries tid + 256j (j < 4) and their row copies, reading the codewords from
   // the (2^Q, 2) table as stage_hyb_col does.
-  auto build_etab = [&](const float (&nw)[V], const float (&sg)[V], float ssk) {
+  auto load_codewords = [&](float (&h)[4][2]) {
     const int ncol = 1 << (P.Q - 3), mask = (1 << P.Q) - 1;
-    float h[4][2];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int k = tid + 256 * j, col = k & 63, i = col + ncol * (k >> 6), ie = i & mask;
@@ -139,6 +138,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
       const float y = col < ncol ? P.table[2 * ie + 1] : 0.0f;
       h[j][1] = (i >> P.Q) ? -y : y;
     }
+  };
+  auto build_etab = [&](const float (&h)[4][2], const float (&nw)[V], const float (&sg)[V], float ssk) {
     float2* et = reinterpret_cast<float2*>(lut);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -253,6 +254,9 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
       // --------------------------- alpha + mu sweep ----------------------------
       float hca[CUA > 0 ? CUA : 1][CUA > 0 ? R : 1][CUA > 0 ? R : 1][V];
       fill_cache(hca, std::integral_constant<int, CUA>{});
+      // kETab: this thread's 4 LUT entries for the per-step tables, held over the sweep
+      float hE[4][2];
+      if constexpr (kETab) load_codewords(hE);
       double C = 0.0;  // C_{t-1}
       int k = 0;
       int rho = nb - KV;  // kV * (t - 1) mod nb at t = 0
@@ -271,7 +275,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           sg[v] = CT::kSigma * gbuf[t * V + v];  // f = g . c = sg . h
         }
         if constexpr (kETab) {  // every wave has left step t-1's table (barrier at its end)
-          build_etab(nw, sg, ssk);
+          build_etab(hE, nw, sg, ssk);
           __syncthreads();
         }
         const uint32_t yb = base_off(rho);
