@@ -99,10 +99,12 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   const int utid = kColUnroll ? (int)col_walk_unit((uint32_t)tid) : tid;
   const Swizzle swz = P.swz;
 
-  // LDS: the (m~, mu) pairs sit at byte 0, so a pair's byte address is 8 times
+  // LDS: the (m~, mu) pairs sit at byte kPairBase (0, or 16 KiB behind the
+  // column walk's tables), so a pair's byte address is kPairBase plus 8 times
   // its element index.
-  float2* mm = reinterpret_cast<float2*>(smem);                    // NT (m~, mu) then (n~, nu)
-  double* cvec = reinterpret_cast<double*>(smem + (size_t)8 * NT);  // N  C_{t-1}
+  constexpr uint32_t kPairBase = kETab ? 16384u : 0u;
+  float2* mm = reinterpret_cast<float2*>(smem + kPairBase);                    // NT (m~, mu) then (n~, nu)
+  double* cvec = reinterpret_cast<double*>(smem + kPairBase + (size_t)8 * NT);  // N  C_{t-1}
   float* wmax = reinterpret_cast<float*>(cvec + ((N + 1) & ~1));    // 2*kMaxWaves
   float* wsum = wmax + 2 * kMaxWaves;                               // 2*kMaxWaves
   // Last wsum word: the block-wide input flag (at most 8 waves use wsum, launch
@@ -111,8 +113,11 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   float* wbuf = wsum + 2 * kMaxWaves;                               // N*V
   float* gbuf = wbuf + N * V;                                       // N*V
   float* apart = gbuf + N * V;                                      // 2*nwaves*(V+1) per-wave partials
-  // HYB: signed LUT (code_hyb_signed) or column-walk LUT (hyb_col_base), 8-byte aligned
-  float* lut = reinterpret_cast<float*>(smem) + ((apart + 2 * nwaves * (V + 1) - reinterpret_cast<float*>(smem) + 1) & ~1);
+  // HYB: signed LUT (code_hyb_signed), 8-byte aligned; kETab: the column walk's
+  // per-step tables at byte 0.
+  float* lut = kETab ? reinterpret_cast<float*>(smem)
+                     : reinterpret_cast<float*>(smem) +
+                           ((apart + 2 * nwaves * (V + 1) - reinterpret_cast<float*>(smem) + 1) & ~1);
 
   if constexpr (CODE == CODE_HYB) {
     stage_hyb_signed(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
@@ -197,7 +202,7 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   auto slot_off = [&](int k, int rho) -> uint32_t {
     return swizzle(rotr_bits((uint32_t)(k * NB), rho, nb), swz) << 3;
   };
-  auto lds_pair = [&](uint32_t off) -> float2& { return *reinterpret_cast<float2*>(smem + off); };
+  auto lds_pair = [&](uint32_t off) -> float2& { return *reinterpret_cast<float2*>(smem + kPairBase + off); };
 
   if (tid == 0) *bflag = 0;
   __syncthreads();
@@ -449,10 +454,19 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         __syncthreads();
       }
 
-      // The beta sweep reads codewords: the LUT replaces the table (every wave
-      // has left it at the last alpha step's barrier; the barriers below come
-      // before the first LUT read).
-      if constexpr (kETab) stage_hyb_col(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
+      // kETab: the beta sweep's table replaces the alpha sweep's (every wave has
+      // left it at the last alpha step's barrier; the barriers below come before
+      // its first read): float4 entry k = (-|d|^2, sg . h, h) of LUT entry k,
+      // rows 0..15 only, its codeword written here and (e, f) per step.  A
+      // state's entry is at twice its codeword's LUT byte, its row wrapped mod 16
+      // (cbs doubled for the sweep).
+      if constexpr (kETab) {
+        float4* et = reinterpret_cast<float4*>(lut);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) et[tid + 256 * j] = make_float4(0.0f, 0.0f, hE[j][0], hE[j][1]);
+#pragma unroll
+        for (int c = 0; c < R; ++c) cbs[c] <<= 1;
+      }
 
       // log2 Z and E[F] = sum_j 2^(m_{N-1}(j) - log2 Z) mu_{N-1}(j); m~ and mu of a
       // state share a pair, so the sums run over pairs.
@@ -523,6 +537,23 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           nw[v] = -wbuf[t * V + v] * sk;
           sg[v] = CT::kSigma * gbuf[t * V + v];
         }
+        if constexpr (kETab) {  // every wave has left step t+1's table (barrier at its end)
+          float4* et = reinterpret_cast<float4*>(lut);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int kk = tid + 256 * j;
+            const float2 h = *reinterpret_cast<const float2*>(&et[kk].z);
+            float e = 0.0f, f = 0.0f;
+            const float d0 = fmaf(h.x, ssk, nw[0]);
+            e = fmaf(-d0, d0, e);
+            f = fmaf(sg[0], h.x, f);
+            const float d1 = fmaf(h.y, ssk, nw[1]);
+            e = fmaf(-d1, d1, e);
+            f = fmaf(sg[1], h.y, f);
+            *reinterpret_cast<float2*>(&et[kk]) = make_float2(e, f);
+          }
+          __syncthreads();
+        }
         const uint32_t yb = base_off(rho);
         uint32_t Ku[UPT], Kk[R];  // uniform per step
 #pragma unroll
@@ -538,6 +569,13 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
             return slot_off(c, rho);
           }
         };
+        // kETab: the table bases, opaque per step, so that the 16 x 16 wrapped
+        // addresses are formed where they are read, not hoisted out of the loop.
+        uint32_t cbo[kETab ? R : 1];
+        if constexpr (kETab) {
+#pragma unroll
+          for (int c = 0; c < R; ++c) cbo[c] = (uint32_t)opaque((int)cbs[c]);
+        }
 
         // Output p of butterfly u: n~ and nu of state p*NB + u from the shifted
         // inputs nr[c] (maximum 0) and raw nu inputs, and the butterfly's
@@ -550,6 +588,14 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
           float y[R], z[R], hh[R][V];
 #pragma unroll
           for (int c = 0; c < R; ++c) {
+            if constexpr (kETab) {
+              const float4 ef = *reinterpret_cast<const float4*>(smem + ((cbo[c] + 2 * hyb_col_step(p, c)) & 0x3FFFu));
+              y[c] = nr[c] + ef.x;
+              z[c] = nui[c] + ef.y;
+              hh[c][0] = ef.z;
+              hh[c][1] = ef.w;
+              continue;
+            }
             if (i < CU) {
 #pragma unroll
               for (int v = 0; v < V; ++v) hh[c][v] = hcb[i < CU ? i : 0][p][c][v];
@@ -757,6 +803,10 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
         if (lane == 0) wmax[(k & 1) * kMaxWaves + wave] = tmax;
         rho = rho - KV < 0 ? rho - KV + nb : rho - KV;
         __syncthreads();
+      }
+      if constexpr (kETab) {  // the alpha sweep's undoubled bases
+#pragma unroll
+        for (int c = 0; c < R; ++c) cbs[c] >>= 1;
       }
     };
     if (Tb < kExactBelowT) {
