@@ -585,6 +585,31 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
                             const float (&nui)[R], float pms, float pmu, float oout, float& no, float& nuo,
                             float& a0, float (&a1)[V]) -> float {
           constexpr bool SHIFT = decltype(shift_tag)::value;
+          if constexpr (kETab && !SHIFT) {
+            // Group-sum variant (M = 0): each input's terms are summed as its
+            // table entry is read, so one entry at a time is live (the same
+            // operations as the general form below).
+            const float Dp = pmu - EFg;
+            float s = 0.0f, ez = 0.0f, ga[V];
+#pragma unroll
+            for (int c = 0; c < R; ++c) {
+              const float4 ef = *reinterpret_cast<const float4*>(smem + ((cbo[c] + 2 * hyb_col_step(p, c)) & 0x3FFFu));
+              const float e = fexp2(nr[c] + ef.x);
+              const float ezc = e * (nui[c] + ef.y);
+              s = c ? s + e : e;
+              ez = c ? ez + ezc : ezc;
+              const float wgt = fmaf(e, Dp, ezc);
+              ga[0] = c ? fmaf(wgt, ef.z, ga[0]) : wgt * ef.z;
+              ga[1] = c ? fmaf(wgt, ef.w, ga[1]) : wgt * ef.w;
+            }
+            const float G = fexp2(pms);
+            a0 = G * fmaf(Dp, s, ez);
+#pragma unroll
+            for (int v = 0; v < V; ++v) a1[v] = G * ga[v];
+            no = flog2(s) + (0.0f - oout);
+            nuo = ez * frcp(s);
+            return s;
+          }
           float y[R], z[R], hh[R][V];
 #pragma unroll
           for (int c = 0; c < R; ++c) {
