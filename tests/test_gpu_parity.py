@@ -712,6 +712,40 @@ def test_qat_shape_batch_spot_check_vs_oracle(bcjr_mod, oracle):
     assert (recon.cpu().numpy()[pick] == recon_r.reshape(len(pick), N * V)).all()
 
 
+def test_column_walk_many_sequences_per_workgroup_mixed_variants(bcjr_mod, oracle):
+    """The column-walk kernels keep per-step tables, the codeword bases and (in
+    the forward) codeword copies in LDS and registers from one sequence to the
+    next of a workgroup.  B = 2048 sequences (about three per resident
+    workgroup) whose T cycles through the group-sum and the exact variants, one
+    with a NaN weight in the middle: late sequences against the oracle (soft,
+    log Z, gradient, Viterbi walk), the NaN one NaN."""
+    _say("column walk, B=2048 mixed T")
+    from bcjr import bcjr_forward_backward, viterbi_encode_v_batched_hip
+    B, N, L, V = 2048, 128, 16, 2
+    rng = np.random.default_rng(17)
+    seq = rng.standard_normal((B, N, V)).astype(np.float32)
+    g = rng.standard_normal((B, N, V)).astype(np.float32)
+    Ts = np.resize(np.array([0.05, 0.3, 1.0, 0.02, 0.1], np.float32), B)
+    bad = 1027
+    seq[bad, 5, 1] = np.nan
+    cb, cb_np = _codebook(bcjr_mod, oracle, "hyb", L, "cuda")
+    x = torch.tensor(seq, device="cuda", requires_grad=True)
+    soft, logZ = bcjr_forward_backward(x, cb, torch.tensor(Ts, device="cuda"), L=L, k=2, V=V)
+    (torch.nan_to_num(soft) * torch.tensor(g, device="cuda")).sum().backward()
+    assert torch.isnan(soft[bad]).all() and torch.isnan(x.grad[bad]).all()
+    for b in (1026, 1028, 1790, 2045, 2046, 2047):
+        s_ref, z_ref = oracle.bcjr_forward(seq[b:b + 1], cb_np, float(Ts[b]), L, 4)
+        d_ref = oracle.bcjr_backward(seq[b:b + 1], cb_np, float(Ts[b]), L, 4, g[b:b + 1])
+        assert max_rel(soft[b:b + 1].detach().cpu().numpy(), s_ref) < SOFT_TOL, b
+        assert abs(float(logZ[b].detach()) - float(z_ref[0])) <= LOGZ_TOL * abs(float(z_ref[0])), b
+        assert max_rel(x.grad[b:b + 1].cpu().numpy(), d_ref) < GRAD_TOL, b
+    good = np.array([1790, 2045, 2046, 2047])
+    _, _, _, _, out = viterbi_encode_v_batched_hip(torch.tensor(seq.reshape(B, N * V), device="cuda"), cb,
+                                                   L=L, k=2, V=V, return_all=True)
+    walk_r = oracle.viterbi(seq[good], cb_np, L, 4)[0]
+    assert np.array_equal(out["walk"].cpu().numpy()[good], walk_r)
+
+
 def test_low_temperature_precision_bound(bcjr_mod, oracle):
     """Below T = 1e-2 float32 log-domain recursions lose precision as 1/T (the
     alpha/beta of a state on the final best path can lie ~1e4/T log2-units below
