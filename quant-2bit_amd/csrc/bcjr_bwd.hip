@@ -122,9 +122,6 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
   if constexpr (CODE == CODE_HYB) {
     stage_hyb_signed(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
     __syncthreads();
-  } else if constexpr (kCol && !kETab) {
-    stage_hyb_col(reinterpret_cast<float2*>(lut), P.table, P.Q, tid, nthr);
-    __syncthreads();
   }
   const unsigned char* lutb = reinterpret_cast<const unsigned char*>(lut);
   // Table of the column-walk alpha + mu sweep, in the LUT's place until the beta
@@ -318,10 +315,6 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
             if (i < CUA) {
 #pragma unroll
               for (int v = 0; v < V; ++v) h[v] = hca[i < CUA ? i : 0][p][r][v];
-            } else if constexpr (kCol) {
-              const float2 cw = hyb_col_read(lutb, cb + hyb_col_step(p, r));
-              h[0] = cw.x;
-              h[1] = cw.y;
             } else {
               raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)r, (uint32_t)(p * NT + R * u + r), P.table,
                                     lut, P.Q, h);
@@ -439,9 +432,8 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
 #pragma unroll kOuterUnroll<R>
               for (int r = 0; r < R; ++r) {
                 float mo, muo;
-                const uint32_t cb = kCol ? hyb_col_base((uint32_t)(R * u + r), P.Q) : 0u;
-                const float s = alpha_out(Fast{}, i, r, xu, u, m, mui, oout, mo, muo, cb);
-                if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, i, r, xu, u, m, mui, oout, mo, muo, cb);
+                const float s = alpha_out(Fast{}, i, r, xu, u, m, mui, oout, mo, muo, 0u);
+                if (!EXACT && s < kUnderflow) alpha_out(std::true_type{}, i, r, xu, u, m, mui, oout, mo, muo, 0u);
                 lds_pair(yi ^ koff(r)) = make_float2(mo, muo);
                 tmax = vmax_raw(tmax, mo);
               }
@@ -624,10 +616,6 @@ __global__ __launch_bounds__(CODE == CODE_HYB_COL ? 256 : 512, CODE == CODE_HYB_
             if (i < CU) {
 #pragma unroll
               for (int v = 0; v < V; ++v) hh[c][v] = hcb[i < CU ? i : 0][p][c][v];
-            } else if constexpr (kCol) {
-              const float2 cw = hyb_col_read(lutb, cbs[c] + hyb_col_step(p, c));
-              hh[c][0] = cw.x;
-              hh[c][1] = cw.y;
             } else {
               raw_codeword<CODE, V>(xu, p * ANT + CT::A * (uint32_t)c, (uint32_t)(p * NT + R * u + c), P.table,
                                     lut, P.Q, hh[c]);
